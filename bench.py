@@ -1,0 +1,227 @@
+"""Grouped FP16 GEMM benchmark on one MI355X.
+
+Headline (the BASELINE metric): grouped TFLOP/s and the fraction of the dense FP16 MFMA peak on the
+mixed-512 set (512 problems, m, n log-uniform in [64, 1024], k log-uniform in [64, 2048], seed 42,
+macro-tile 128x64x32), for all four sort modes, next to the per-problem-launch baseline, the static
+tail share and the measured tail idle.  A step is one executor.run() over the whole set with every
+operand already resident in HBM.  `value` is the best sort mode's throughput.
+
+Prints one JSON line.  --gpus above 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_PEAK_TFLOPS = 2516.6   # dense fp16 MFMA, MI355X (AMD public spec)
+HBM_PEAK_GBS = 8000.0       # HBM3E, MI355X (AMD public spec)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="mixed512",
+                    choices=["plumbing16", "mixed512", "dense64", "moe64", "longtail4096"])
+    ap.add_argument("--config", default=None, help="macro-tile, default: the workload's")
+    ap.add_argument("--modes", default="0,1,2,3", help="sort modes to time")
+    ap.add_argument("--no-baseline", action="store_true", help="skip the per-problem-launch baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
+    ap.add_argument("--fma", action="store_true", help="FMA tile path instead of MFMA")
+    ap.add_argument("--table", action="store_true", help="also print the reference-style results table")
+    return ap.parse_args()
+
+
+def time_runs(torch, fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` calls after `warmup`, HIP events on the current stream."""
+    for _ in range(warmup):
+        st = fn()
+        if st != 0:
+            raise RuntimeError(f"hipError_t {st}")
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        st = fn()
+        if st != 0:
+            raise RuntimeError(f"hipError_t {st}")
+    stop.record()
+    stop.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def measured_tail_idle(torch, ex) -> float:
+    """Share of workgroup time spent idle after finishing its last tile while others still run:
+    sum_w (T_end - end_w) / (W * (T_end - T_start)), from per-workgroup wall clocks."""
+    grid = ex.grid_ctas()
+    clock = torch.zeros(2 * grid, dtype=torch.int64, device="cuda")
+    st = ex.run_traced(0, clock.data_ptr())
+    if st != 0:
+        raise RuntimeError(f"traced run hipError_t {st}")
+    torch.cuda.synchronize()
+    c = clock.cpu().numpy().reshape(grid, 2).astype("float64")
+    t0, t1 = c[:, 0].min(), c[:, 1].max()
+    if t1 <= t0:
+        return 0.0
+    return float(((t1 - c[:, 1]).sum()) / (grid * (t1 - t0)))
+
+
+def cpu_baseline(dw, spec, seconds: float):
+    """The oracle's FP32 host GEMM (OpenMP form of the reference's loop, bit-identical to it) on a
+    bounded prefix of the same problems, on this host's cores."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    done_flops, elapsed, used = 0.0, 0.0, 0
+    order = list(range(spec.count))
+    for i in order:
+        m, n, k = int(spec.m[i]), int(spec.n[i]), int(spec.k[i])
+        if m <= 0 or n <= 0:
+            continue
+        a, b, c = dw.host_a(i), dw.host_b(i), dw.host_c(i)
+        t0 = time.perf_counter()
+        O.gemm(m, n, k, a, max(1, k), b, max(1, n), c, max(1, n), float(spec.alpha[i]), float(spec.beta[i]),
+               threads=threads)
+        elapsed += time.perf_counter() - t0
+        done_flops += 2.0 * m * n * k
+        used += 1
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(done_flops / elapsed / 1e12, 6) if elapsed > 0 else None,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first {used} of {spec.count} problems of the same set ({done_flops / 1e9:.1f} GFLOP, "
+                  f"{elapsed:.1f} s), oracle FP32 host GEMM, OpenMP over rows, {threads} threads",
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the grouped GEMM shards "
+              "problems across GPUs with no exchange step, see the design notes.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from grouped_gemm_gpu_kernel_amd import api
+    from grouped_gemm_gpu_kernel_amd.api import GroupedGemmExecutor, KernelConfig, SortMode
+    from grouped_gemm_gpu_kernel_amd.workloads import DeviceWorkload, make_spec
+
+    torch.cuda.set_device(0)
+    spec = make_spec(args.workload)
+    config_name = args.config or spec.config
+    cfg = KernelConfig.named(config_name, use_tensor_cores=not args.fma)
+    dw = DeviceWorkload(spec)
+    probs = dw.problems()
+    flops = spec.flops()
+    algo_bytes = spec.algorithmic_bytes()
+    print(f"# workload {spec.name}: {spec.count} problems, {flops / 1e9:.2f} GFLOP, "
+          f"{algo_bytes / 1e9:.3f} GB algorithmic, config {config_name}", file=sys.stderr, flush=True)
+
+    modes = [SortMode(int(x)) for x in args.modes.split(",")]
+    per_mode = []
+    best = None
+    stream = torch.cuda.current_stream()
+    for mode in modes:
+        t0 = time.perf_counter()
+        prep = api.prepare_problem_set(probs, cfg, mode)
+        ex = GroupedGemmExecutor()
+        st = ex.build(prep, cfg)
+        if st != 0:
+            raise RuntimeError(f"build hipError_t {st}")
+        prep_ms = (time.perf_counter() - t0) * 1e3
+        ms = time_runs(torch, lambda: ex.run(stream), args.steps, args.warmup)
+        tail_idle = measured_tail_idle(torch, ex)
+        row = {
+            "mode": api.sort_mode_name(mode), "prep_ms": round(prep_ms, 3), "kernel_ms": round(ms, 4),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "tiles": prep.total_tiles,
+            "grid_ctas": ex.grid_ctas(), "launches": 1,
+            "tail_share": round(api.tail_work_share(prep, cfg), 4), "tail_idle_measured": round(tail_idle, 4),
+        }
+        per_mode.append(row)
+        print(f"# {row}", file=sys.stderr, flush=True)
+        if best is None or ms < best[1]:
+            best = (row, ms)
+        ex.close()
+
+    baseline = None
+    if not args.no_baseline:
+        bsteps = max(1, min(args.steps, 20))
+        bms = time_runs(torch, lambda: api.run_baseline_per_problem(probs, cfg, stream), bsteps, 2)
+        baseline = {"mode": "baseline_per_problem", "kernel_ms": round(bms, 4),
+                    "tflops": round(flops / (bms * 1e-3) / 1e12, 3),
+                    "launches": api.count_non_empty_problems(probs, cfg)}
+        print(f"# {baseline}", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds)
+
+    row, ms = best
+    tflops = flops / (ms * 1e-3) / 1e12
+    achieved_gbs = algo_bytes / (ms * 1e-3) / 1e9
+    mfma_frac = tflops / MFMA_PEAK_TFLOPS
+    hbm_frac = achieved_gbs / HBM_PEAK_GBS
+    ridge = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    bound = "hbm" if flops / algo_bytes < ridge else "mfma"
+    if bound == "hbm":
+        roofline = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(hbm_frac, 4), "traffic": None}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(mfma_frac, 4), "traffic": None}
+    out = {
+        "metric": "grouped TFLOP/s + % FP16 MFMA peak on mixed-512, 1 MI355X; tail_share",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 in, fp32 accumulate",
+        "data": "synthetic (seeded; shapes from numpy RandomState, operands from a counter hash on the GPU)",
+        "config": {"workload": spec.name, "problems": spec.count, "cta": config_name,
+                   "path": "fma" if args.fma else "mfma", "best_sort_mode": row["mode"],
+                   "gflop": round(flops / 1e9, 3), "algorithmic_gb": round(algo_bytes / 1e9, 4)},
+        "mfma_peak_frac": round(mfma_frac, 4),
+        "hbm_roofline_frac": round(hbm_frac, 4),
+        "tail_share": row["tail_share"],
+        "tail_idle_measured": row["tail_idle_measured"],
+        "per_mode": per_mode,
+        "baseline_per_problem": baseline,
+        "speedup_vs_per_problem_baseline": round(baseline["kernel_ms"] / ms, 2) if baseline else None,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if args.table:
+        print(f"{'mode':24}{'prep_ms':>10}{'kernel_ms':>11}{'tflops':>10}{'tiles':>8}{'grid':>7}{'launches':>10}"
+              f"{'tail_share':>12}", file=sys.stderr)
+        for r in per_mode + ([baseline] if baseline else []):
+            print(f"{r['mode']:24}{r.get('prep_ms', 0):>10.3f}{r['kernel_ms']:>11.4f}{r['tflops']:>10.2f}"
+                  f"{r.get('tiles', 0):>8}{r.get('grid_ctas', 0):>7}{r['launches']:>10}{r.get('tail_share', 0):>12.4f}",
+                  file=sys.stderr)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

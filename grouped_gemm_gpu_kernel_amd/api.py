@@ -1,0 +1,276 @@
+"""Python view of the grouped GEMM API.
+
+Same names, fields and error behaviour as the reference's C++ API
+(include/grouped_gemm/grouped_gemm.cuh): functions return hipError_t status
+codes as ints (0 = success) where the reference returns cudaError_t, and
+problems carry raw device pointers.  Everything runs in the HIP library
+through its C-ABI (include/grouped_gemm_amd.h).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field, fields
+from enum import IntEnum
+from typing import Optional, Sequence
+
+from . import _lib
+from ._lib import GGKernelConfig, GGOccupancyInfo, GGProblemDesc
+
+
+class SortMode(IntEnum):
+    """include/grouped_gemm/grouped_gemm.cuh:11-16"""
+    kNone = 0
+    kByK = 1
+    kByTiles = 2
+    kByTilesThenK = 3
+
+
+@dataclass
+class ProblemDesc:
+    """include/grouped_gemm/grouped_gemm.cuh:18-35.  a, b: device pointers to
+    binary16 row-major A[m x lda], B[k x ldb]; c (0/None allowed), d: float32."""
+    m: int
+    n: int
+    k: int
+    a: int
+    b: int
+    c: Optional[int]
+    d: int
+    lda: int
+    ldb: int
+    ldc: int
+    ldd: int
+    alpha: float = 1.0
+    beta: float = 0.0
+
+    def to_c(self) -> GGProblemDesc:
+        return GGProblemDesc(self.m, self.n, self.k, self.a or None, self.b or None, self.c or None,
+                             self.d or None, self.lda, self.ldb, self.ldc, self.ldd, self.alpha, self.beta)
+
+    @staticmethod
+    def from_c(p: GGProblemDesc) -> "ProblemDesc":
+        return ProblemDesc(p.m, p.n, p.k, p.a or 0, p.b or 0, p.c or None, p.d or 0, p.lda, p.ldb, p.ldc, p.ldd,
+                           p.alpha, p.beta)
+
+
+@dataclass
+class KernelConfig:
+    """include/grouped_gemm/grouped_gemm.cuh:37-45"""
+    cta_m: int = 64
+    cta_n: int = 64
+    cta_k: int = 16
+    threads: int = 256
+    persistent_ctas: int = 0
+    use_tensor_cores: bool = True
+
+    def to_c(self) -> GGKernelConfig:
+        return GGKernelConfig(self.cta_m, self.cta_n, self.cta_k, self.threads, self.persistent_ctas,
+                              1 if self.use_tensor_cores else 0)
+
+    @staticmethod
+    def named(name: str, **kw) -> "KernelConfig":
+        """'64x64x16', '128x64x32' or '64x128x32' (bench/benchmark_grouped_gemm.cu:112-234)."""
+        m, n, k = (int(x) for x in name.split("x"))
+        return KernelConfig(cta_m=m, cta_n=n, cta_k=k, **kw)
+
+
+@dataclass
+class PreparedProblemSet:
+    """include/grouped_gemm/grouped_gemm.cuh:47-52"""
+    sorted_problems: list = field(default_factory=list)
+    sorted_to_original: list = field(default_factory=list)
+    tile_offsets: list = field(default_factory=lambda: [0])
+    total_tiles: int = 0
+
+
+@dataclass
+class OccupancyInfo:
+    """include/grouped_gemm/grouped_gemm.cuh:54-83 plus the gfx950 register split."""
+    sm_count: int = 0
+    max_blocks_per_sm: int = 0
+    active_blocks_per_sm: int = 0
+    threads_per_block: int = 0
+    max_threads_per_sm: int = 0
+    warps_per_block: int = 0
+    max_warps_per_sm: int = 0
+    active_warps_per_sm: int = 0
+    max_registers_per_sm: int = 0
+    max_registers_per_block: int = 0
+    estimated_registers_per_thread: int = 0
+    estimated_registers_per_block: int = 0
+    registers_per_thread: int = 0
+    registers_per_block: int = 0
+    register_limited_blocks_per_sm: int = 0
+    static_shared_bytes: int = 0
+    dynamic_shared_bytes: int = 0
+    theoretical_occupancy: float = 0.0
+    using_tensor_cores: bool = False
+    vgprs_per_thread: int = 0
+    agprs_per_thread: int = 0
+    sgprs_per_wave: int = 0
+    scratch_bytes_per_thread: int = 0
+    lds_limited_blocks_per_sm: int = 0
+    wave_limited_blocks_per_sm: int = 0
+
+
+def _problem_array(problems: Sequence[ProblemDesc]):
+    arr = (GGProblemDesc * max(1, len(problems)))()
+    for i, p in enumerate(problems):
+        arr[i] = p.to_c()
+    return arr
+
+
+def _stream_handle(stream) -> Optional[int]:
+    """Accepts None, an int hipStream_t, or a torch.cuda.Stream."""
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream or None
+    return stream.cuda_stream or None
+
+
+def sort_mode_name(sort_mode: int) -> str:
+    """src/grouped_gemm.cu:952-965"""
+    return _lib.lib().gg_sort_mode_name(int(sort_mode)).decode()
+
+
+def tile_count_for_problem(problem: ProblemDesc, config: KernelConfig) -> int:
+    """src/grouped_gemm.cu:54-65"""
+    return _lib.lib().gg_tile_count(ctypes.byref(problem.to_c()), ctypes.byref(config.to_c()))
+
+
+def prepare_problem_set(problems: Sequence[ProblemDesc], config: KernelConfig,
+                        sort_mode: int) -> PreparedProblemSet:
+    """src/grouped_gemm.cu:967-1022 (host only, no GPU use)."""
+    count = len(problems)
+    arr = _problem_array(problems)
+    out = (GGProblemDesc * max(1, count))()
+    perm = (ctypes.c_int * max(1, count))()
+    offsets = (ctypes.c_int * (count + 1))()
+    total = _lib.lib().gg_prepare_problem_set(arr, count, ctypes.byref(config.to_c()), int(sort_mode), out,
+                                              perm, offsets)
+    if total < 0:
+        raise ValueError("gg_prepare_problem_set rejected its arguments")
+    return PreparedProblemSet(
+        sorted_problems=[ProblemDesc.from_c(out[i]) for i in range(count)],
+        sorted_to_original=[perm[i] for i in range(count)],
+        tile_offsets=[offsets[i] for i in range(count + 1)],
+        total_tiles=total,
+    )
+
+
+def query_occupancy(config: KernelConfig, info: Optional[OccupancyInfo] = None):
+    """src/grouped_gemm.cu:1024-1083.  Returns (status, OccupancyInfo)."""
+    raw = GGOccupancyInfo()
+    status = _lib.lib().gg_query_occupancy(ctypes.byref(config.to_c()), ctypes.byref(raw))
+    info = info if info is not None else OccupancyInfo()
+    if status == _lib.HIP_SUCCESS:
+        for f in fields(OccupancyInfo):
+            value = getattr(raw, f.name)
+            setattr(info, f.name, bool(value) if f.name == "using_tensor_cores" else value)
+    return status, info
+
+
+class GroupedGemmExecutor:
+    """include/grouped_gemm/grouped_gemm.cuh:94-115 (src/grouped_gemm.cu:1085-1277)."""
+
+    def __init__(self):
+        self._handle = _lib.lib().gg_executor_create()
+        if not self._handle:
+            raise MemoryError("gg_executor_create failed")
+
+    def close(self) -> None:
+        if self._handle:
+            _lib.lib().gg_executor_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def build(self, prepared: PreparedProblemSet, config: KernelConfig) -> int:
+        count = len(prepared.sorted_problems)
+        arr = _problem_array(prepared.sorted_problems)
+        offs = (ctypes.c_int * max(1, len(prepared.tile_offsets)))(*prepared.tile_offsets)
+        return _lib.lib().gg_executor_build(self._handle, arr, count, offs, len(prepared.tile_offsets),
+                                            prepared.total_tiles, ctypes.byref(config.to_c()))
+
+    def run(self, stream=None) -> int:
+        return _lib.lib().gg_executor_run(self._handle, _stream_handle(stream))
+
+    def run_traced(self, tile_map_ptr: int = 0, wg_clock_ptr: int = 0, stream=None) -> int:
+        """Scheduler with instrumentation: tile_map_ptr (device int[3*total_tiles]) receives
+        (problem, tile_m, tile_n) per tile instead of computing; wg_clock_ptr (device
+        int64[2*grid]) receives each workgroup's start/end wall clock (100 MHz)."""
+        return _lib.lib().gg_executor_run_traced(self._handle, tile_map_ptr or None, wg_clock_ptr or None,
+                                                 _stream_handle(stream))
+
+    def problem_count(self) -> int:
+        return _lib.lib().gg_executor_problem_count(self._handle)
+
+    def total_tiles(self) -> int:
+        return _lib.lib().gg_executor_total_tiles(self._handle)
+
+    def grid_ctas(self) -> int:
+        return _lib.lib().gg_executor_grid_ctas(self._handle)
+
+    def using_tensor_cores(self) -> bool:
+        return bool(_lib.lib().gg_executor_using_tensor_cores(self._handle))
+
+
+def run_grouped_gemm_once(problems: Sequence[ProblemDesc], sort_mode: int, config: KernelConfig,
+                          stream=None) -> int:
+    """src/grouped_gemm.cu:1279-1291"""
+    arr = _problem_array(problems)
+    return _lib.lib().gg_run_grouped_gemm_once(arr, len(problems), int(sort_mode), ctypes.byref(config.to_c()),
+                                               _stream_handle(stream))
+
+
+def run_baseline_per_problem(problems: Sequence[ProblemDesc], config: KernelConfig, stream=None) -> int:
+    """src/grouped_gemm.cu:1293-1317"""
+    arr = _problem_array(problems)
+    return _lib.lib().gg_run_baseline_per_problem(arr, len(problems), ctypes.byref(config.to_c()),
+                                                  _stream_handle(stream))
+
+
+def count_non_empty_problems(problems: Sequence[ProblemDesc], config: KernelConfig) -> int:
+    """src/grouped_gemm.cu:1319-1329"""
+    arr = _problem_array(problems)
+    return _lib.lib().gg_count_non_empty_problems(arr, len(problems), ctypes.byref(config.to_c()))
+
+
+def grid_ctas_for(config: KernelConfig, total_tiles: int) -> int:
+    """Persistent grid size build() chooses on this device (src/grouped_gemm.cu:1228-1236)."""
+    value = _lib.lib().gg_grid_ctas_for(ctypes.byref(config.to_c()), total_tiles)
+    if value < 0:
+        raise _lib.HipError(-value, "gg_grid_ctas_for")
+    return value
+
+
+def total_flops(problems: Sequence[ProblemDesc]) -> float:
+    """sum of 2*m*n*k (bench/benchmark_grouped_gemm.cu:570-576)."""
+    return float(sum(2.0 * p.m * p.n * p.k for p in problems))
+
+
+def tail_work_share(prepared: PreparedProblemSet, config: KernelConfig) -> float:
+    """Static tail share (bench/benchmark_grouped_gemm.cu:580-607): work = tiles * ceil(k / cta_k)
+    per problem in sorted order; the share of the last max(1, count // 10) problems."""
+    n = len(prepared.sorted_problems)
+    if n == 0:
+        return 0.0
+    tail = max(1, n // 10)
+    total = tail_w = 0.0
+    for i, p in enumerate(prepared.sorted_problems):
+        w = float(prepared.tile_offsets[i + 1] - prepared.tile_offsets[i]) * ((p.k + config.cta_k - 1) // config.cta_k)
+        total += w
+        if i >= n - tail:
+            tail_w += w
+    return tail_w / total if total > 0 else 0.0

@@ -1,0 +1,245 @@
+// c_api.cpp -- extern "C" facade (include/grouped_gemm_amd.h) over the C++ API.
+//
+// Each entry point converts plain structs to the C++ types, calls the
+// namespace grouped_gemm function of the same name and returns its hipError_t
+// as int.  No exception crosses this boundary.
+#include "grouped_gemm_amd.h"
+
+#include <cstddef>
+#include <new>
+#include <vector>
+
+#include "grouped_gemm/grouped_gemm.h"
+
+namespace gg = grouped_gemm;
+
+// gg_problem_desc and grouped_gemm::ProblemDesc must stay layout-identical.
+static_assert(sizeof(gg_problem_desc) == sizeof(gg::ProblemDesc), "ProblemDesc layout");
+static_assert(offsetof(gg_problem_desc, a) == offsetof(gg::ProblemDesc, a), "ProblemDesc.a");
+static_assert(offsetof(gg_problem_desc, d) == offsetof(gg::ProblemDesc, d), "ProblemDesc.d");
+static_assert(offsetof(gg_problem_desc, ldd) == offsetof(gg::ProblemDesc, ldd), "ProblemDesc.ldd");
+static_assert(offsetof(gg_problem_desc, beta) == offsetof(gg::ProblemDesc, beta), "ProblemDesc.beta");
+
+struct gg_executor {
+  gg::GroupedGemmExecutor executor;
+};
+
+namespace {
+
+gg::ProblemDesc to_cpp(const gg_problem_desc& p) {
+  gg::ProblemDesc out{};
+  out.m = p.m;
+  out.n = p.n;
+  out.k = p.k;
+  out.a = static_cast<const __half*>(p.a);
+  out.b = static_cast<const __half*>(p.b);
+  out.c = p.c;
+  out.d = p.d;
+  out.lda = p.lda;
+  out.ldb = p.ldb;
+  out.ldc = p.ldc;
+  out.ldd = p.ldd;
+  out.alpha = p.alpha;
+  out.beta = p.beta;
+  return out;
+}
+
+gg_problem_desc to_c(const gg::ProblemDesc& p) {
+  gg_problem_desc out{};
+  out.m = p.m;
+  out.n = p.n;
+  out.k = p.k;
+  out.a = p.a;
+  out.b = p.b;
+  out.c = p.c;
+  out.d = p.d;
+  out.lda = p.lda;
+  out.ldb = p.ldb;
+  out.ldc = p.ldc;
+  out.ldd = p.ldd;
+  out.alpha = p.alpha;
+  out.beta = p.beta;
+  return out;
+}
+
+gg::KernelConfig to_cpp(const gg_kernel_config& c) {
+  gg::KernelConfig out;
+  out.cta_m = c.cta_m;
+  out.cta_n = c.cta_n;
+  out.cta_k = c.cta_k;
+  out.threads = c.threads;
+  out.persistent_ctas = c.persistent_ctas;
+  out.use_tensor_cores = c.use_tensor_cores != 0;
+  return out;
+}
+
+std::vector<gg::ProblemDesc> to_cpp(const gg_problem_desc* problems, int count) {
+  std::vector<gg::ProblemDesc> out;
+  if (count > 0 && problems != nullptr) {
+    out.reserve(count);
+    for (int i = 0; i < count; ++i) out.push_back(to_cpp(problems[i]));
+  }
+  return out;
+}
+
+bool bad_list(const gg_problem_desc* problems, int count) {
+  return count < 0 || (count > 0 && problems == nullptr);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gg_version(void) { return "grouped_gemm_amd 0.1 gfx950"; }
+
+const char* gg_sort_mode_name(int sort_mode) {
+  return gg::sort_mode_name(static_cast<gg::SortMode>(sort_mode));
+}
+
+int gg_tile_count(const gg_problem_desc* problem, const gg_kernel_config* config) {
+  if (problem == nullptr || config == nullptr) return 0;
+  return gg::tile_count_for_problem(to_cpp(*problem), to_cpp(*config));
+}
+
+int gg_prepare_problem_set(const gg_problem_desc* problems, int count, const gg_kernel_config* config,
+                           int sort_mode, gg_problem_desc* sorted_problems, int* sorted_to_original,
+                           int* tile_offsets) {
+  if (config == nullptr || bad_list(problems, count)) return -1;
+  try {
+    const gg::PreparedProblemSet prepared =
+        gg::prepare_problem_set(to_cpp(problems, count), to_cpp(*config), static_cast<gg::SortMode>(sort_mode));
+    for (int i = 0; i < count; ++i) {
+      if (sorted_problems != nullptr) sorted_problems[i] = to_c(prepared.sorted_problems[i]);
+      if (sorted_to_original != nullptr) sorted_to_original[i] = prepared.sorted_to_original[i];
+    }
+    if (tile_offsets != nullptr) {
+      for (int i = 0; i <= count; ++i) tile_offsets[i] = prepared.tile_offsets[i];
+    }
+    return prepared.total_tiles;
+  } catch (...) {
+    return -1;
+  }
+}
+
+int gg_query_occupancy(const gg_kernel_config* config, gg_occupancy_info* info) {
+  if (config == nullptr || info == nullptr) return hipErrorInvalidValue;
+  gg::OccupancyInfo o;
+  const hipError_t status = gg::query_occupancy(to_cpp(*config), &o);
+  if (status != hipSuccess) return status;
+  info->sm_count = o.sm_count;
+  info->max_blocks_per_sm = o.max_blocks_per_sm;
+  info->active_blocks_per_sm = o.active_blocks_per_sm;
+  info->threads_per_block = o.threads_per_block;
+  info->max_threads_per_sm = o.max_threads_per_sm;
+  info->warps_per_block = o.warps_per_block;
+  info->max_warps_per_sm = o.max_warps_per_sm;
+  info->active_warps_per_sm = o.active_warps_per_sm;
+  info->max_registers_per_sm = o.max_registers_per_sm;
+  info->max_registers_per_block = o.max_registers_per_block;
+  info->estimated_registers_per_thread = o.estimated_registers_per_thread;
+  info->estimated_registers_per_block = o.estimated_registers_per_block;
+  info->registers_per_thread = o.registers_per_thread;
+  info->registers_per_block = o.registers_per_block;
+  info->register_limited_blocks_per_sm = o.register_limited_blocks_per_sm;
+  info->static_shared_bytes = o.static_shared_bytes;
+  info->dynamic_shared_bytes = o.dynamic_shared_bytes;
+  info->theoretical_occupancy = o.theoretical_occupancy;
+  info->using_tensor_cores = o.using_tensor_cores ? 1 : 0;
+  info->vgprs_per_thread = o.vgprs_per_thread;
+  info->agprs_per_thread = o.agprs_per_thread;
+  info->sgprs_per_wave = o.sgprs_per_wave;
+  info->scratch_bytes_per_thread = o.scratch_bytes_per_thread;
+  info->lds_limited_blocks_per_sm = o.lds_limited_blocks_per_sm;
+  info->wave_limited_blocks_per_sm = o.wave_limited_blocks_per_sm;
+  return hipSuccess;
+}
+
+gg_executor* gg_executor_create(void) { return new (std::nothrow) gg_executor(); }
+
+void gg_executor_destroy(gg_executor* executor) { delete executor; }
+
+int gg_executor_build(gg_executor* executor, const gg_problem_desc* sorted_problems, int count,
+                      const int* tile_offsets, int offsets_len, int total_tiles,
+                      const gg_kernel_config* config) {
+  if (executor == nullptr) return hipErrorInvalidDevicePointer;
+  if (config == nullptr || bad_list(sorted_problems, count) || offsets_len < 0 ||
+      (offsets_len > 0 && tile_offsets == nullptr)) {
+    return hipErrorInvalidValue;
+  }
+  try {
+    gg::PreparedProblemSet prepared;
+    prepared.sorted_problems = to_cpp(sorted_problems, count);
+    prepared.sorted_to_original.resize(count);
+    for (int i = 0; i < count; ++i) prepared.sorted_to_original[i] = i;
+    prepared.tile_offsets.assign(tile_offsets, tile_offsets + offsets_len);
+    prepared.total_tiles = total_tiles;
+    if (prepared.tile_offsets.empty()) return hipErrorInvalidValue;
+    return executor->executor.build(prepared, to_cpp(*config));
+  } catch (...) {
+    return hipErrorOutOfMemory;
+  }
+}
+
+int gg_executor_run(const gg_executor* executor, hipStream_t stream) {
+  if (executor == nullptr) return hipErrorInvalidDevicePointer;
+  return executor->executor.run(stream);
+}
+
+int gg_executor_run_traced(const gg_executor* executor, int* d_tile_map, long long* d_wg_clock,
+                           hipStream_t stream) {
+  if (executor == nullptr) return hipErrorInvalidDevicePointer;
+  return executor->executor.run_traced(d_tile_map, d_wg_clock, stream);
+}
+
+int gg_executor_problem_count(const gg_executor* executor) {
+  return executor != nullptr ? executor->executor.problem_count() : 0;
+}
+
+int gg_executor_total_tiles(const gg_executor* executor) {
+  return executor != nullptr ? executor->executor.total_tiles() : 0;
+}
+
+int gg_executor_grid_ctas(const gg_executor* executor) {
+  return executor != nullptr ? executor->executor.grid_ctas() : 0;
+}
+
+int gg_executor_using_tensor_cores(const gg_executor* executor) {
+  return executor != nullptr && executor->executor.using_tensor_cores() ? 1 : 0;
+}
+
+int gg_run_grouped_gemm_once(const gg_problem_desc* problems, int count, int sort_mode,
+                             const gg_kernel_config* config, hipStream_t stream) {
+  if (config == nullptr || bad_list(problems, count)) return hipErrorInvalidValue;
+  try {
+    return gg::run_grouped_gemm_once(to_cpp(problems, count), static_cast<gg::SortMode>(sort_mode),
+                                     to_cpp(*config), stream);
+  } catch (...) {
+    return hipErrorOutOfMemory;
+  }
+}
+
+int gg_run_baseline_per_problem(const gg_problem_desc* problems, int count, const gg_kernel_config* config,
+                                hipStream_t stream) {
+  if (config == nullptr || bad_list(problems, count)) return hipErrorInvalidValue;
+  try {
+    return gg::run_baseline_per_problem(to_cpp(problems, count), to_cpp(*config), stream);
+  } catch (...) {
+    return hipErrorOutOfMemory;
+  }
+}
+
+int gg_count_non_empty_problems(const gg_problem_desc* problems, int count, const gg_kernel_config* config) {
+  if (config == nullptr || bad_list(problems, count)) return 0;
+  return gg::count_non_empty_problems(to_cpp(problems, count), to_cpp(*config));
+}
+
+int gg_grid_ctas_for(const gg_kernel_config* config, int total_tiles) {
+  if (config == nullptr) return -static_cast<int>(hipErrorInvalidValue);
+  const gg::KernelConfig cfg = to_cpp(*config);
+  gg::OccupancyInfo o;
+  const hipError_t status = gg::query_occupancy(cfg, &o);
+  if (status != hipSuccess) return -static_cast<int>(status);
+  return gg::grid_ctas_for(total_tiles, cfg, o);
+}
+
+}  // extern "C"

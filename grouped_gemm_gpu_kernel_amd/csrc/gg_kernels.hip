@@ -1,0 +1,428 @@
+// gg_kernels.hip -- gfx950 kernels of the grouped FP16 GEMM and the thin C-ABI
+// (grouped_gemm_amd_kernels.h) the C++ host runtime calls.
+//
+// Kernels:
+//   gg_grouped_kernel  persistent scheduler (grouped_gemm_kernel,
+//                      src/grouped_gemm.cu:640-675): one launch, workgroups
+//                      claim tile indices from a device-wide counter until all
+//                      total_tiles are taken; each index is mapped to
+//                      (problem, tile_m, tile_n) by a search over tile_offsets.
+//   gg_single_kernel   one problem, one workgroup per tile
+//                      (single_problem_gemm_kernel, src/grouped_gemm.cu:677-688).
+//   fill kernels       synthetic inputs and output poisoning for tests/benches.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <string.h>
+
+#include "gg_common.h"
+#include "gg_tiles.h"
+#include "grouped_gemm_amd_kernels.h"
+
+// Compiler resource table of this build (generated from the compiler's
+// resource-usage report; see gg_resources.cpp).
+extern "C" int gg_compiler_resources(int kind, int variant, int path, int* vgprs, int* agprs,
+                                     int* sgprs, int* scratch, int* waves_per_simd, int* lds);
+
+namespace gg {
+
+typedef const GG_CONST int* const_int_ptr;
+typedef const GG_CONST uint32_t* const_u32_ptr;
+
+// Reads descriptor `index` with a wave-uniform index from memory no thread
+// writes during the launch, so the compiler can use scalar loads.
+__device__ __forceinline__ gg_device_problem_desc load_problem(const gg_device_problem_desc* problems,
+                                                               int index) {
+  static_assert(sizeof(gg_device_problem_desc) % 4 == 0, "descriptor is whole dwords");
+  constexpr int kWords = sizeof(gg_device_problem_desc) / 4;
+  const_u32_ptr src = (const_u32_ptr)(problems + index);
+  struct Words { uint32_t w[kWords]; } words;
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) words.w[i] = src[i];
+  return __builtin_bit_cast(gg_device_problem_desc, words);
+}
+
+struct GroupedArgs {
+  const gg_device_problem_desc* __restrict__ problems;
+  const int* __restrict__ offsets;
+  int count;
+  int total;
+  int* state;          // [0] claim counter, [1] retired workgroups
+  int* tile_map;       // traced launches only
+  long long* wg_clock; // traced launches only
+};
+
+// Index of the problem that owns tile t: the number of problems p with
+// offsets[p + 1] <= t, i.e. upper_bound over offsets[1..count] -- the same
+// function as find_problem_by_tile (src/grouped_gemm.cu:219-234).  Problems
+// with zero tiles never own an index.
+//
+// Evaluated by the whole wave at once: each step tests 64 evenly spaced
+// candidates in parallel and keeps the span between the last true and the
+// first false one, so count <= 4096 takes one coarse and one exact step (two
+// dependent loads) instead of log2(count) serial probes.  The result is
+// wave-uniform.
+__device__ __forceinline__ int find_problem(const int* __restrict__ offsets, int count, int t) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int lo = 0;
+  int hi = count;  // the answer lies in [lo, hi]; candidates p in [lo, hi)
+  while (hi - lo > kWave) {
+    const int step = (hi - lo + kWave - 1) / kWave;
+    const int p = lo + (lane + 1) * step - 1;
+    const bool below = (p < hi) && (offsets[p + 1] <= t);
+    const int passed = __popcll(__ballot(below));
+    const int next_lo = lo + passed * step;
+    const int probe_false = lo + (passed + 1) * step - 1;
+    hi = probe_false < hi ? probe_false : hi;
+    lo = next_lo;
+  }
+  const int p = lo + lane;
+  const bool below = (p < hi) && (offsets[p + 1] <= t);
+  return __builtin_amdgcn_readfirstlane(lo + __popcll(__ballot(below)));
+}
+
+template <int V, int PATH, bool TRACED>
+__global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) {
+  using G = typename VariantGeometry<V>::type;
+  using Tile = typename TileFor<PATH, G>::type;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
+  __shared__ int s_claim;
+
+  const int tid = threadIdx.x;
+  long long clock_start = 0;
+  long long clock_end = 0;
+  if (TRACED) {
+    clock_start = wall_clock64();
+    clock_end = clock_start;
+  }
+
+  int next = 0;
+  if (tid == 0) s_claim = atomicAdd(args.state, 1);
+  __syncthreads();
+  int t = __builtin_amdgcn_readfirstlane(s_claim);
+  while (t < args.total) {
+    // Claim the next index now; its latency hides behind this tile's work.
+    if (tid == 0) next = atomicAdd(args.state, 1);
+
+    const int prob = find_problem(args.offsets, args.count, t);
+    // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
+    const gg_device_problem_desc p = load_problem(args.problems, prob);
+    const int local = t - ((const_int_ptr)args.offsets)[prob];
+    if (p.tiles_n > 0) {
+      const int tile_m = local / p.tiles_n;
+      const int tile_n = local - tile_m * p.tiles_n;
+      if (tile_m < p.tiles_m) {
+        if (TRACED && args.tile_map != nullptr) {
+          if (tid == 0) {
+            args.tile_map[3 * t + 0] = prob;
+            args.tile_map[3 * t + 1] = tile_m;
+            args.tile_map[3 * t + 2] = tile_n;
+          }
+        } else {
+          Tile::run(p, tile_m, tile_n, lds);
+        }
+      }
+    }
+    if (TRACED) clock_end = wall_clock64();
+
+    __syncthreads();  // every thread has read s_claim for this round
+    if (tid == 0) s_claim = next;
+    __syncthreads();
+    t = __builtin_amdgcn_readfirstlane(s_claim);
+  }
+
+  if (tid == 0) {
+    if (TRACED && args.wg_clock != nullptr) {
+      args.wg_clock[2 * blockIdx.x + 0] = clock_start;
+      args.wg_clock[2 * blockIdx.x + 1] = clock_end;
+    }
+    // Every workgroup makes exactly one claim past the end before it retires,
+    // so the last one to retire knows no claim is still in flight and returns
+    // the state to zero for the next launch in stream order.
+    const int retired = atomicAdd(args.state + 1, 1);
+    if (retired == (int)gridDim.x - 1) {
+      atomicExch(args.state + 0, 0);
+      atomicExch(args.state + 1, 0);
+    }
+  }
+}
+
+template <int V, int PATH>
+__global__ __launch_bounds__(kThreads) void gg_single_kernel(gg_device_problem_desc p) {
+  using G = typename VariantGeometry<V>::type;
+  using Tile = typename TileFor<PATH, G>::type;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
+  const int t = blockIdx.x;
+  if (p.tiles_n <= 0 || t >= p.tiles_m * p.tiles_n) return;
+  const int tile_m = t / p.tiles_n;
+  const int tile_n = t - tile_m * p.tiles_n;
+  Tile::run(p, tile_m, tile_n, lds);
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data: a counter-based hash (splitmix64 finaliser) so that element i
+// depends only on (seed, stream, i) and any element can be recomputed alone.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  x ^= x >> 31;
+  return x;
+}
+
+__device__ __forceinline__ float unit_draw(uint64_t key, uint64_t i) {
+  const uint64_t h = mix64(key + i * 0x9e3779b97f4a7c15ull);
+  return (float)(h >> 40) * 5.9604644775390625e-08f;  // [0, 1) in steps of 2^-24
+}
+
+__global__ void fill_uniform_f16_kernel(uint16_t* dst, int64_t count, uint64_t key, float lo, float span) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const _Float16 h = (_Float16)(lo + span * unit_draw(key, (uint64_t)i));
+    dst[i] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
+__global__ void fill_uniform_f32_kernel(float* dst, int64_t count, uint64_t key, float lo, float span) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    dst[i] = lo + span * unit_draw(key, (uint64_t)i);
+  }
+}
+
+__global__ void fill_normal_f16_kernel(uint16_t* dst, int64_t count, uint64_t key, float sigma) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float u1 = 1.0f - unit_draw(key, 2 * (uint64_t)i);  // (0, 1]
+    const float u2 = unit_draw(key, 2 * (uint64_t)i + 1);
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    const _Float16 h = (_Float16)(sigma * z);
+    dst[i] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
+__global__ void fill_f32_kernel(float* dst, int64_t count, float value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    dst[i] = value;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel tables: [variant][path] (and [traced] for the grouped kernel).
+// ---------------------------------------------------------------------------
+using GroupedFn = void (*)(GroupedArgs);
+using SingleFn = void (*)(gg_device_problem_desc);
+
+template <int V, int P>
+struct KernelEntry {
+  static constexpr GroupedFn grouped = gg_grouped_kernel<V, P, false>;
+  static constexpr GroupedFn traced = gg_grouped_kernel<V, P, true>;
+  static constexpr SingleFn single = gg_single_kernel<V, P>;
+};
+
+#define GG_ROW(V) \
+  {{KernelEntry<V, 0>::grouped, KernelEntry<V, 0>::traced, KernelEntry<V, 0>::single}, \
+   {KernelEntry<V, 1>::grouped, KernelEntry<V, 1>::traced, KernelEntry<V, 1>::single}}
+
+struct KernelSet {
+  GroupedFn grouped;
+  GroupedFn traced;
+  SingleFn single;
+};
+
+static const KernelSet kKernels[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {
+    GG_ROW(GGK_VARIANT_64x64x16), GG_ROW(GGK_VARIANT_128x64x32), GG_ROW(GGK_VARIANT_64x128x32)};
+#undef GG_ROW
+
+static bool valid_kernel(int variant, int path) {
+  return variant >= 0 && variant < GGK_VARIANT_COUNT && path >= 0 && path < GGK_PATH_COUNT;
+}
+
+static hipError_t fill_launch_shape(int64_t count, dim3* grid) {
+  if (count < 0) return hipErrorInvalidValue;
+  int64_t blocks = (count + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  *grid = dim3((unsigned)blocks);
+  return hipSuccess;
+}
+
+static uint64_t fill_key(uint64_t seed, uint64_t stream_id) {
+  return mix64(seed ^ mix64(stream_id + 0x632be59bd9b4e019ull));
+}
+
+}  // namespace gg
+
+using namespace gg;
+
+extern "C" {
+
+hipError_t ggk_alloc(void** ptr, size_t bytes) {
+  if (ptr == nullptr) return hipErrorInvalidValue;
+  return hipMalloc(ptr, bytes);
+}
+
+hipError_t ggk_free(void* ptr) { return ptr == nullptr ? hipSuccess : hipFree(ptr); }
+
+hipError_t ggk_copy_to_device(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return hipSuccess;
+  return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+hipError_t ggk_copy_to_host(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return hipSuccess;
+  return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
+hipError_t ggk_zero(void* ptr, size_t bytes) {
+  if (bytes == 0) return hipSuccess;
+  return hipMemset(ptr, 0, bytes);
+}
+
+hipError_t ggk_stream_synchronize(hipStream_t stream) { return hipStreamSynchronize(stream); }
+
+hipError_t ggk_device_synchronize(void) { return hipDeviceSynchronize(); }
+
+hipError_t ggk_device_info_get(ggk_device_info* out) {
+  if (out == nullptr) return hipErrorInvalidValue;
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return st;
+  hipDeviceProp_t prop;
+  st = hipGetDeviceProperties(&prop, device);
+  if (st != hipSuccess) return st;
+  memset(out, 0, sizeof(*out));
+  out->device = device;
+  out->compute_units = prop.multiProcessorCount;
+  out->max_threads_per_cu = prop.maxThreadsPerMultiProcessor;
+  out->max_wgs_per_cu = prop.maxBlocksPerMultiProcessor;
+  out->wave_size = prop.warpSize;
+  out->regs_per_cu = prop.regsPerMultiprocessor;
+  out->regs_per_block = prop.regsPerBlock;
+  out->lds_per_cu = (int)prop.maxSharedMemoryPerMultiProcessor;
+  out->lds_per_block = (int)prop.sharedMemPerBlock;
+  out->l2_bytes = prop.l2CacheSize;
+  out->clock_khz = prop.clockRate;
+  out->major = prop.major;
+  out->minor = prop.minor;
+  strncpy(out->arch_name, prop.gcnArchName, sizeof(out->arch_name) - 1);
+  return hipSuccess;
+}
+
+hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
+                              const int* d_tile_offsets, int problem_count, int total_tiles,
+                              int* d_state, int grid, hipStream_t stream) {
+  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
+    return hipErrorInvalidValue;
+  }
+  if (total_tiles == 0 || problem_count == 0) return hipSuccess;
+  if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
+    return hipErrorInvalidDevicePointer;
+  }
+  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, nullptr, nullptr};
+  void* params[] = {&args};
+  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].grouped), dim3(grid),
+                         dim3(kThreads), params, 0, stream);
+}
+
+hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
+                                     const int* d_tile_offsets, int problem_count, int total_tiles,
+                                     int* d_state, int grid, int* d_tile_map, long long* d_wg_clock,
+                                     hipStream_t stream) {
+  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
+    return hipErrorInvalidValue;
+  }
+  if (total_tiles == 0 || problem_count == 0) return hipSuccess;
+  if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
+    return hipErrorInvalidDevicePointer;
+  }
+  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, d_tile_map, d_wg_clock};
+  void* params[] = {&args};
+  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].traced), dim3(grid),
+                         dim3(kThreads), params, 0, stream);
+}
+
+hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,
+                             hipStream_t stream) {
+  if (!valid_kernel(variant, path) || problem == nullptr) return hipErrorInvalidValue;
+  const int64_t tiles = (int64_t)problem->tiles_m * problem->tiles_n;
+  if (tiles <= 0) return hipSuccess;
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  gg_device_problem_desc p = *problem;
+  void* params[] = {&p};
+  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].single), dim3((unsigned)tiles),
+                         dim3(kThreads), params, 0, stream);
+}
+
+hipError_t ggk_kernel_resources_get(int kernel_kind, int variant, int path, ggk_kernel_resources* out) {
+  if (!valid_kernel(variant, path) || out == nullptr) return hipErrorInvalidValue;
+  if (kernel_kind != GGK_KERNEL_GROUPED && kernel_kind != GGK_KERNEL_SINGLE) return hipErrorInvalidValue;
+  memset(out, 0, sizeof(*out));
+  gg_compiler_resources(kernel_kind, variant, path, &out->vgprs, &out->agprs, &out->sgprs,
+                        &out->scratch_bytes_per_lane, &out->compiler_waves_per_simd, &out->lds_bytes);
+  const void* fn = kernel_kind == GGK_KERNEL_GROUPED
+                       ? reinterpret_cast<const void*>(kKernels[variant][path].grouped)
+                       : reinterpret_cast<const void*>(kKernels[variant][path].single);
+  hipFuncAttributes attr;
+  hipError_t st = hipFuncGetAttributes(&attr, fn);
+  if (st != hipSuccess) return st;
+  out->num_regs = attr.numRegs;
+  out->lds_static = (int)attr.sharedSizeBytes;
+  out->lds_dynamic = 0;
+  out->local_bytes = (int)attr.localSizeBytes;
+  out->max_threads = attr.maxThreadsPerBlock;
+  return hipSuccess;
+}
+
+hipError_t ggk_occupancy(int variant, int path, int* active_wgs_per_cu) {
+  if (!valid_kernel(variant, path) || active_wgs_per_cu == nullptr) return hipErrorInvalidValue;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      active_wgs_per_cu, reinterpret_cast<const void*>(kKernels[variant][path].grouped), kThreads, 0);
+}
+
+hipError_t ggk_fill_uniform_f16(void* d_dst, int64_t count, uint64_t seed, uint64_t stream_id, float lo,
+                                float hi, hipStream_t stream) {
+  dim3 grid;
+  hipError_t st = fill_launch_shape(count, &grid);
+  if (st != hipSuccess || count == 0) return st;
+  if (d_dst == nullptr) return hipErrorInvalidDevicePointer;
+  hipLaunchKernelGGL(fill_uniform_f16_kernel, grid, dim3(256), 0, stream, static_cast<uint16_t*>(d_dst),
+                     count, fill_key(seed, stream_id), lo, hi - lo);
+  return hipGetLastError();
+}
+
+hipError_t ggk_fill_uniform_f32(float* d_dst, int64_t count, uint64_t seed, uint64_t stream_id, float lo,
+                                float hi, hipStream_t stream) {
+  dim3 grid;
+  hipError_t st = fill_launch_shape(count, &grid);
+  if (st != hipSuccess || count == 0) return st;
+  if (d_dst == nullptr) return hipErrorInvalidDevicePointer;
+  hipLaunchKernelGGL(fill_uniform_f32_kernel, grid, dim3(256), 0, stream, d_dst, count,
+                     fill_key(seed, stream_id), lo, hi - lo);
+  return hipGetLastError();
+}
+
+hipError_t ggk_fill_normal_f16(void* d_dst, int64_t count, uint64_t seed, uint64_t stream_id, float sigma,
+                               hipStream_t stream) {
+  dim3 grid;
+  hipError_t st = fill_launch_shape(count, &grid);
+  if (st != hipSuccess || count == 0) return st;
+  if (d_dst == nullptr) return hipErrorInvalidDevicePointer;
+  hipLaunchKernelGGL(fill_normal_f16_kernel, grid, dim3(256), 0, stream, static_cast<uint16_t*>(d_dst),
+                     count, fill_key(seed, stream_id), sigma);
+  return hipGetLastError();
+}
+
+hipError_t ggk_fill_f32(float* d_dst, int64_t count, float value, hipStream_t stream) {
+  dim3 grid;
+  hipError_t st = fill_launch_shape(count, &grid);
+  if (st != hipSuccess || count == 0) return st;
+  if (d_dst == nullptr) return hipErrorInvalidDevicePointer;
+  hipLaunchKernelGGL(fill_f32_kernel, grid, dim3(256), 0, stream, d_dst, count, value);
+  return hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,424 @@
+// grouped_gemm.cpp -- host runtime of the grouped FP16 GEMM (C++ API of
+// include/grouped_gemm/grouped_gemm.h).
+//
+// Plain C++17: every GPU interaction goes through the thin kernel C-ABI
+// (grouped_gemm_amd_kernels.h).  Reference counterparts: src/grouped_gemm.cu
+// host section (:912-1331) and the variant/occupancy model (:47-217).
+#include "grouped_gemm/grouped_gemm.h"
+
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+#include <tuple>
+#include <utility>
+
+namespace grouped_gemm {
+namespace {
+
+constexpr int kThreadsPerBlock = 256;
+constexpr int kWaveSize = 64;
+// gfx950: 512 registers per lane per SIMD shared by VGPRs and AGPRs, allocated
+// in blocks of 8; at most 8 waves per SIMD.
+constexpr int kRegsPerLanePerSimd = 512;
+constexpr int kRegAllocGranule = 8;
+constexpr int kMaxWavesPerSimd = 8;
+
+int ceil_div(int x, int y) { return (x + y - 1) / y; }
+
+// The three accepted shapes (resolve_variant, src/grouped_gemm.cu:67-81).
+int resolve_variant(const KernelConfig& config) {
+  if (config.threads != kThreadsPerBlock) return -1;
+  if (config.cta_m == 64 && config.cta_n == 64 && config.cta_k == 16) return GGK_VARIANT_64x64x16;
+  if (config.cta_m == 128 && config.cta_n == 64 && config.cta_k == 32) return GGK_VARIANT_128x64x32;
+  if (config.cta_m == 64 && config.cta_n == 128 && config.cta_k == 32) return GGK_VARIANT_64x128x32;
+  return -1;
+}
+
+struct RuntimeMode {
+  int variant = -1;
+  int path = GGK_PATH_FMA;
+  ggk_device_info device{};
+};
+
+// resolve_runtime_mode (src/grouped_gemm.cu:111-143): unsupported shapes are
+// InvalidValue; the MFMA path is used when requested.  The library is built
+// for gfx950 only, where every accepted shape has an MFMA kernel.
+hipError_t resolve_runtime_mode(const KernelConfig& config, RuntimeMode* mode) {
+  const int variant = resolve_variant(config);
+  if (variant < 0) return hipErrorInvalidValue;
+  const hipError_t status = ggk_device_info_get(&mode->device);
+  if (status != hipSuccess) return status;
+  mode->variant = variant;
+  mode->path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;
+  return hipSuccess;
+}
+
+// Formula estimate of registers per lane (the role of
+// estimated_*_registers_per_thread, src/grouped_gemm.cu:175-217), for this
+// build's tiles.  MFMA: the (BM*BN/256) float accumulators a lane holds, its
+// A/B operand fragments (4 registers per 32-row or 32-column block), the
+// staged global pieces (7 registers each) and ~24 for addresses and loop state.
+// FMA: RM*RN accumulators, RM 16-byte A slices, RN B values, staging, ~24.
+int estimated_registers_per_thread(const KernelConfig& config, bool mfma) {
+  const int bm = config.cta_m;
+  const int bn = config.cta_n;
+  const int bk = 32;  // internal stage depth of every variant
+  const int pieces = (bm * bk / 8 + bk * bn / 8) / kThreadsPerBlock;
+  const int staging = pieces * 7;
+  if (mfma) {
+    const int acc = bm * bn / kThreadsPerBlock;
+    const int fragments = 4 * (bm / 64) + 4 * (bn / 64);
+    return acc + fragments + staging + 24;
+  }
+  const int rm = bm / 16;
+  const int rn = bn / 16;
+  return rm * rn + rm * 4 + rn + staging + 24;
+}
+
+int round_up(int x, int granule) { return (x + granule - 1) / granule * granule; }
+
+hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, OccupancyInfo* info) {
+  const ggk_device_info& dev = mode.device;
+  const bool mfma = mode.path == GGK_PATH_MFMA;
+  *info = OccupancyInfo{};
+  info->sm_count = dev.compute_units;
+  info->max_blocks_per_sm = dev.max_wgs_per_cu;
+  info->threads_per_block = kThreadsPerBlock;
+  info->max_threads_per_sm = dev.max_threads_per_cu;
+  info->warps_per_block = kThreadsPerBlock / (dev.wave_size > 0 ? dev.wave_size : kWaveSize);
+  info->max_warps_per_sm = dev.max_threads_per_cu / (dev.wave_size > 0 ? dev.wave_size : kWaveSize);
+  info->max_registers_per_sm = dev.regs_per_cu;
+  info->max_registers_per_block = dev.regs_per_block;
+  info->estimated_registers_per_thread = estimated_registers_per_thread(config, mfma);
+  info->estimated_registers_per_block = info->estimated_registers_per_thread * kThreadsPerBlock;
+  info->using_tensor_cores = mfma;
+
+  ggk_kernel_resources res{};
+  hipError_t status = ggk_kernel_resources_get(GGK_KERNEL_GROUPED, mode.variant, mode.path, &res);
+  if (status != hipSuccess) return status;
+  status = ggk_occupancy(mode.variant, mode.path, &info->active_blocks_per_sm);
+  if (status != hipSuccess) return status;
+
+  info->vgprs_per_thread = res.vgprs;
+  info->agprs_per_thread = res.agprs;
+  info->sgprs_per_wave = res.sgprs;
+  info->scratch_bytes_per_thread = res.scratch_bytes_per_lane;
+  // VGPRs and AGPRs come from one register file; when the compiler report is
+  // unavailable, fall back to what hipFuncGetAttributes reports.
+  const int regs = (res.vgprs + res.agprs) > 0 ? res.vgprs + res.agprs : res.num_regs;
+  info->registers_per_thread = regs;
+  info->registers_per_block = regs * kThreadsPerBlock;
+  info->static_shared_bytes = res.lds_static > 0 ? res.lds_static : res.lds_bytes;
+  info->dynamic_shared_bytes = res.lds_dynamic;
+
+  // A workgroup's 4 waves sit one per SIMD, so resident workgroups per CU are
+  // limited by waves per SIMD (registers), by LDS and by the wave slots.
+  const int waves_per_simd =
+      regs > 0 ? std::min(kMaxWavesPerSimd, kRegsPerLanePerSimd / round_up(regs, kRegAllocGranule))
+               : kMaxWavesPerSimd;
+  info->register_limited_blocks_per_sm = std::min(info->max_blocks_per_sm, waves_per_simd);
+  const int lds_per_block = info->static_shared_bytes + info->dynamic_shared_bytes;
+  info->lds_limited_blocks_per_sm =
+      lds_per_block > 0 ? dev.lds_per_cu / lds_per_block : info->max_blocks_per_sm;
+  info->wave_limited_blocks_per_sm =
+      info->warps_per_block > 0 ? info->max_warps_per_sm / info->warps_per_block : 0;
+
+  info->active_warps_per_sm = info->active_blocks_per_sm * info->warps_per_block;
+  if (info->max_warps_per_sm > 0) {
+    info->theoretical_occupancy =
+        static_cast<float>(info->active_warps_per_sm) / static_cast<float>(info->max_warps_per_sm);
+  }
+  return hipSuccess;
+}
+
+void release(DeviceProblemDesc*& problems, int*& offsets, int*& state) {
+  if (problems == nullptr && offsets == nullptr && state == nullptr) return;
+  // Launches on any stream may still read these buffers: finish them first.
+  ggk_device_synchronize();
+  ggk_free(problems);
+  ggk_free(offsets);
+  ggk_free(state);
+  problems = nullptr;
+  offsets = nullptr;
+  state = nullptr;
+}
+
+}  // namespace
+
+// Grid size (src/grouped_gemm.cu:1228-1236): the requested persistent size,
+// else every resident workgroup slot but no more than max(total_tiles, CUs).
+int grid_ctas_for(int total_tiles, const KernelConfig& config, const OccupancyInfo& occupancy) {
+  if (total_tiles <= 0) return 0;
+  int grid;
+  if (config.persistent_ctas > 0) {
+    grid = config.persistent_ctas;
+  } else {
+    const int resident = occupancy.sm_count * std::max(1, occupancy.active_blocks_per_sm);
+    grid = std::min(resident, std::max(total_tiles, occupancy.sm_count));
+  }
+  return std::max(1, grid);
+}
+
+int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& config) {
+  if (problem.m <= 0 || problem.n <= 0 || config.cta_m <= 0 || config.cta_n <= 0) return 0;
+  return ceil_div(problem.m, config.cta_m) * ceil_div(problem.n, config.cta_n);
+}
+
+DeviceProblemDesc to_device_problem(const ProblemDesc& p, const KernelConfig& config) {
+  DeviceProblemDesc out{};
+  out.m = p.m;
+  out.n = p.n;
+  out.k = p.k;
+  out.a = p.a;
+  out.b = p.b;
+  out.c = p.c;
+  out.d = p.d;
+  out.lda = p.lda;
+  out.ldb = p.ldb;
+  out.ldc = p.ldc;
+  out.ldd = p.ldd;
+  out.alpha = p.alpha;
+  out.beta = p.beta;
+  const bool empty = p.m <= 0 || p.n <= 0 || config.cta_m <= 0 || config.cta_n <= 0;
+  out.tiles_m = empty ? 0 : ceil_div(p.m, config.cta_m);
+  out.tiles_n = empty ? 0 : ceil_div(p.n, config.cta_n);
+  return out;
+}
+
+const char* sort_mode_name(SortMode sort_mode) {
+  switch (sort_mode) {
+    case SortMode::kNone:
+      return "none";
+    case SortMode::kByK:
+      return "sort_by_k";
+    case SortMode::kByTiles:
+      return "sort_by_tiles";
+    case SortMode::kByTilesThenK:
+      return "sort_by_tiles_then_k";
+  }
+  return "unknown";
+}
+
+// prepare_problem_set (src/grouped_gemm.cu:967-1022).  The permutation must
+// equal the reference's std::stable_sort bit for bit, so the orderings are the
+// reference's: by K = larger k first, ties by larger int64 m*n; by tiles = more
+// tiles first, ties by the by-K order.  kByTilesThenK orders exactly like
+// kByTiles, as in the reference (:1000-1005).  Ties keep input order.
+PreparedProblemSet prepare_problem_set(const std::vector<ProblemDesc>& problems,
+                                       const KernelConfig& config, SortMode sort_mode) {
+  const int count = static_cast<int>(problems.size());
+  struct Key {
+    int tiles;
+    int k;
+    int64_t area;
+  };
+  std::vector<Key> keys(count);
+  for (int i = 0; i < count; ++i) {
+    keys[i] = Key{tile_count_for_problem(problems[i], config), problems[i].k,
+                  static_cast<int64_t>(problems[i].m) * problems[i].n};
+  }
+
+  PreparedProblemSet prepared;
+  prepared.sorted_to_original.resize(count);
+  std::iota(prepared.sorted_to_original.begin(), prepared.sorted_to_original.end(), 0);
+  const bool tiles_first = sort_mode == SortMode::kByTiles || sort_mode == SortMode::kByTilesThenK;
+  if (sort_mode == SortMode::kByK || tiles_first) {
+    // Descending lexicographic order on (tiles if tiles_first, k, area).
+    std::stable_sort(prepared.sorted_to_original.begin(), prepared.sorted_to_original.end(),
+                     [&keys, tiles_first](int lhs, int rhs) {
+                       const Key& l = keys[lhs];
+                       const Key& r = keys[rhs];
+                       if (tiles_first && l.tiles != r.tiles) return l.tiles > r.tiles;
+                       return std::tie(l.k, l.area) > std::tie(r.k, r.area);
+                     });
+  }
+
+  prepared.sorted_problems.reserve(count);
+  prepared.tile_offsets.assign(1, 0);
+  prepared.tile_offsets.reserve(count + 1);
+  for (int idx : prepared.sorted_to_original) {
+    prepared.sorted_problems.push_back(problems[idx]);
+    prepared.tile_offsets.push_back(prepared.tile_offsets.back() + keys[idx].tiles);
+  }
+  prepared.total_tiles = prepared.tile_offsets.back();
+  return prepared;
+}
+
+hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info) {
+  if (info == nullptr) return hipErrorInvalidValue;
+  RuntimeMode mode;
+  const hipError_t status = resolve_runtime_mode(config, &mode);
+  if (status != hipSuccess) return status;
+  return fill_occupancy(config, mode, info);
+}
+
+struct GroupedGemmExecutor::Impl {
+  DeviceProblemDesc* d_problems = nullptr;
+  int* d_tile_offsets = nullptr;
+  int* d_state = nullptr;
+
+  int problem_count = 0;
+  int total_tiles = 0;
+  int grid_ctas = 0;
+
+  KernelConfig config{};
+  int variant = -1;
+  int path = GGK_PATH_FMA;
+};
+
+GroupedGemmExecutor::GroupedGemmExecutor() : impl_(new Impl()) {}
+
+GroupedGemmExecutor::~GroupedGemmExecutor() {
+  if (impl_ != nullptr) {
+    release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
+    delete impl_;
+    impl_ = nullptr;
+  }
+}
+
+GroupedGemmExecutor::GroupedGemmExecutor(GroupedGemmExecutor&& other) noexcept : impl_(other.impl_) {
+  other.impl_ = nullptr;
+}
+
+GroupedGemmExecutor& GroupedGemmExecutor::operator=(GroupedGemmExecutor&& other) noexcept {
+  if (this != &other) {
+    if (impl_ != nullptr) {
+      release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
+      delete impl_;
+    }
+    impl_ = other.impl_;
+    other.impl_ = nullptr;
+  }
+  return *this;
+}
+
+// build (src/grouped_gemm.cu:1132-1239).  Beyond the reference's checks it
+// verifies that tile_offsets is the prefix sum of the sorted problems' tile
+// counts, so that a launch can never address a tile outside its problem.
+hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const KernelConfig& config) {
+  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+
+  RuntimeMode mode;
+  hipError_t status = resolve_runtime_mode(config, &mode);
+  if (status != hipSuccess) return status;
+
+  const int problem_count = static_cast<int>(prepared.sorted_problems.size());
+  if (static_cast<int>(prepared.tile_offsets.size()) != problem_count + 1) return hipErrorInvalidValue;
+  if (prepared.tile_offsets.back() != prepared.total_tiles) return hipErrorInvalidValue;
+
+  release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
+  impl_->problem_count = problem_count;
+  impl_->total_tiles = prepared.total_tiles;
+  impl_->grid_ctas = 0;
+  impl_->config = config;
+  impl_->variant = mode.variant;
+  impl_->path = mode.path;
+
+  std::vector<DeviceProblemDesc> device_problems;
+  device_problems.reserve(problem_count);
+  if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
+  for (int i = 0; i < problem_count; ++i) {
+    const ProblemDesc& p = prepared.sorted_problems[i];
+    if (p.m < 0 || p.n < 0 || p.k < 0) return hipErrorInvalidValue;
+    if (p.a == nullptr || p.b == nullptr || p.d == nullptr) return hipErrorInvalidDevicePointer;
+    const DeviceProblemDesc dp = to_device_problem(p, config);
+    const int64_t tiles = static_cast<int64_t>(dp.tiles_m) * dp.tiles_n;
+    if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
+      return hipErrorInvalidValue;
+    }
+    device_problems.push_back(dp);
+  }
+
+  if (problem_count > 0) {
+    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems),
+                       problem_count * sizeof(DeviceProblemDesc));
+    if (status != hipSuccess) return status;
+    status = ggk_copy_to_device(impl_->d_problems, device_problems.data(),
+                                problem_count * sizeof(DeviceProblemDesc));
+    if (status != hipSuccess) return status;
+    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_tile_offsets), (problem_count + 1) * sizeof(int));
+    if (status != hipSuccess) return status;
+    status = ggk_copy_to_device(impl_->d_tile_offsets, prepared.tile_offsets.data(),
+                                (problem_count + 1) * sizeof(int));
+    if (status != hipSuccess) return status;
+  }
+  if (impl_->total_tiles > 0) {
+    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_state), GGK_SCHEDULER_STATE_INTS * sizeof(int));
+    if (status != hipSuccess) return status;
+    status = ggk_zero(impl_->d_state, GGK_SCHEDULER_STATE_INTS * sizeof(int));
+    if (status != hipSuccess) return status;
+  }
+
+  OccupancyInfo occupancy{};
+  status = fill_occupancy(config, mode, &occupancy);
+  if (status != hipSuccess) return status;
+  impl_->grid_ctas = grid_ctas_for(impl_->total_tiles, config, occupancy);
+  return hipSuccess;
+}
+
+// run (src/grouped_gemm.cu:1241-1265).  No counter reset is launched: the
+// grouped kernel returns its scheduler state to zero when its last workgroup
+// retires, so consecutive runs in stream order start from zero.
+hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
+  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
+  return ggk_launch_grouped(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
+                            impl_->problem_count, impl_->total_tiles, impl_->d_state, impl_->grid_ctas, stream);
+}
+
+hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
+  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
+  return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
+                                   impl_->problem_count, impl_->total_tiles, impl_->d_state,
+                                   impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
+}
+
+int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }
+
+int GroupedGemmExecutor::total_tiles() const { return impl_ != nullptr ? impl_->total_tiles : 0; }
+
+int GroupedGemmExecutor::grid_ctas() const { return impl_ != nullptr ? impl_->grid_ctas : 0; }
+
+bool GroupedGemmExecutor::using_tensor_cores() const {
+  return impl_ != nullptr && impl_->path == GGK_PATH_MFMA;
+}
+
+// run_grouped_gemm_once (src/grouped_gemm.cu:1279-1291).
+hipError_t run_grouped_gemm_once(const std::vector<ProblemDesc>& problems, SortMode sort_mode,
+                                 const KernelConfig& config, hipStream_t stream) {
+  const PreparedProblemSet prepared = prepare_problem_set(problems, config, sort_mode);
+  GroupedGemmExecutor executor;
+  hipError_t status = executor.build(prepared, config);
+  if (status != hipSuccess) return status;
+  status = executor.run(stream);
+  if (status != hipSuccess) return status;
+  return ggk_stream_synchronize(stream);
+}
+
+// run_baseline_per_problem (src/grouped_gemm.cu:1293-1317): one launch per
+// problem with tiles; a null a, b or d on any problem is InvalidDevicePointer.
+hipError_t run_baseline_per_problem(const std::vector<ProblemDesc>& problems, const KernelConfig& config,
+                                    hipStream_t stream) {
+  RuntimeMode mode;
+  hipError_t status = resolve_runtime_mode(config, &mode);
+  if (status != hipSuccess) return status;
+  for (const ProblemDesc& p : problems) {
+    if (p.a == nullptr || p.b == nullptr || p.d == nullptr) return hipErrorInvalidDevicePointer;
+    const DeviceProblemDesc dp = to_device_problem(p, config);
+    status = ggk_launch_single(mode.variant, mode.path, &dp, stream);
+    if (status != hipSuccess) return status;
+  }
+  return hipSuccess;
+}
+
+// count_non_empty_problems (src/grouped_gemm.cu:1319-1329).
+int count_non_empty_problems(const std::vector<ProblemDesc>& problems, const KernelConfig& config) {
+  int count = 0;
+  for (const ProblemDesc& p : problems) {
+    if (tile_count_for_problem(p, config) > 0) ++count;
+  }
+  return count;
+}
+
+}  // namespace grouped_gemm

@@ -1,0 +1,194 @@
+// grouped_gemm.h -- C++ host API of the MI355X grouped FP16 GEMM.
+//
+// Drop-in for include/grouped_gemm/grouped_gemm.cuh of the reference: the same
+// namespace, names, fields, defaults and semantics, with HIP types in place of
+// CUDA ones (hipError_t, hipStream_t, __half from <hip/hip_fp16.h>).
+//
+// Each batch computes, for every problem p, D_p = alpha_p * A_p * B_p + beta_p * C_p
+// with A_p [m x k] and B_p [k x n] row-major binary16, C_p / D_p [m x n]
+// row-major float32, and float32 accumulation.  C is read only when c != nullptr
+// and beta != 0.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "grouped_gemm_amd_kernels.h"
+
+namespace grouped_gemm {
+
+// include/grouped_gemm/grouped_gemm.cuh:11-16
+enum class SortMode {
+  kNone = 0,
+  kByK = 1,
+  kByTiles = 2,
+  kByTilesThenK = 3,
+};
+
+// include/grouped_gemm/grouped_gemm.cuh:18-35
+struct ProblemDesc {
+  int m;
+  int n;
+  int k;
+
+  const __half* a;
+  const __half* b;
+  const float* c;
+  float* d;
+
+  int lda;
+  int ldb;
+  int ldc;
+  int ldd;
+
+  float alpha = 1.0f;
+  float beta = 0.0f;
+};
+
+// include/grouped_gemm/grouped_gemm.cuh:37-45.  Accepted shapes, as in the
+// reference: threads == 256 and (cta_m, cta_n, cta_k) one of (64, 64, 16),
+// (128, 64, 32), (64, 128, 32).  use_tensor_cores selects the MFMA tile path;
+// false selects the FMA tile path.
+struct KernelConfig {
+  int cta_m = 64;
+  int cta_n = 64;
+  int cta_k = 16;
+  int threads = 256;
+
+  int persistent_ctas = 0;
+  bool use_tensor_cores = true;
+};
+
+// include/grouped_gemm/grouped_gemm.cuh:47-52
+struct PreparedProblemSet {
+  std::vector<ProblemDesc> sorted_problems;
+  std::vector<int> sorted_to_original;
+  std::vector<int> tile_offsets;
+  int total_tiles = 0;
+};
+
+// include/grouped_gemm/grouped_gemm.cuh:54-83.  "sm" reads "compute unit" and
+// "warp" reads "wavefront" (64 lanes) on this GPU.  The fields after
+// using_tensor_cores are additions that report the gfx950 register split.
+struct OccupancyInfo {
+  int sm_count = 0;
+  int max_blocks_per_sm = 0;
+  int active_blocks_per_sm = 0;
+
+  int threads_per_block = 0;
+  int max_threads_per_sm = 0;
+  int warps_per_block = 0;
+  int max_warps_per_sm = 0;
+  int active_warps_per_sm = 0;
+
+  int max_registers_per_sm = 0;
+  int max_registers_per_block = 0;
+
+  // Formula estimate from the tile shape and the MFMA accumulator layout.
+  int estimated_registers_per_thread = 0;
+  int estimated_registers_per_block = 0;
+
+  // Measured on the compiled kernel: VGPRs + AGPRs per lane.
+  int registers_per_thread = 0;
+  int registers_per_block = 0;
+  int register_limited_blocks_per_sm = 0;
+
+  int static_shared_bytes = 0;
+  int dynamic_shared_bytes = 0;
+
+  float theoretical_occupancy = 0.0f;
+  bool using_tensor_cores = false;
+
+  // gfx950 additions.
+  int vgprs_per_thread = 0;
+  int agprs_per_thread = 0;
+  int sgprs_per_wave = 0;
+  int scratch_bytes_per_thread = 0;
+  int lds_limited_blocks_per_sm = 0;
+  int wave_limited_blocks_per_sm = 0;
+};
+
+// DeviceProblemDesc (src/grouped_gemm.cu:25-45): ProblemDesc plus tiles_m and
+// tiles_n, as the kernels read it.
+using DeviceProblemDesc = gg_device_problem_desc;
+
+// include/grouped_gemm/grouped_gemm.cuh:85-88
+PreparedProblemSet prepare_problem_set(
+    const std::vector<ProblemDesc>& problems,
+    const KernelConfig& config,
+    SortMode sort_mode);
+
+// include/grouped_gemm/grouped_gemm.cuh:90
+const char* sort_mode_name(SortMode sort_mode);
+
+// include/grouped_gemm/grouped_gemm.cuh:92
+hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info);
+
+// include/grouped_gemm/grouped_gemm.cuh:94-115.  build() uploads the sorted
+// descriptors and tile offsets once; run() launches one persistent grid on the
+// given stream.  Not thread-safe: runs of one executor must not overlap (they
+// share one scheduler state).  Device buffers are released on destruction,
+// move-assignment and rebuild, after a device synchronisation.
+class GroupedGemmExecutor {
+ public:
+  GroupedGemmExecutor();
+  ~GroupedGemmExecutor();
+
+  GroupedGemmExecutor(const GroupedGemmExecutor&) = delete;
+  GroupedGemmExecutor& operator=(const GroupedGemmExecutor&) = delete;
+
+  GroupedGemmExecutor(GroupedGemmExecutor&& other) noexcept;
+  GroupedGemmExecutor& operator=(GroupedGemmExecutor&& other) noexcept;
+
+  hipError_t build(const PreparedProblemSet& prepared, const KernelConfig& config);
+  hipError_t run(hipStream_t stream = nullptr) const;
+
+  int problem_count() const;
+  int total_tiles() const;
+  int grid_ctas() const;
+
+  // Additions for measurement and parity checks.  run_traced() runs the same
+  // scheduler with instrumentation (see ggk_launch_grouped_traced).
+  hipError_t run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream = nullptr) const;
+  bool using_tensor_cores() const;
+
+ private:
+  struct Impl;
+  Impl* impl_;
+};
+
+// include/grouped_gemm/grouped_gemm.cuh:117-121.  Synchronises the stream
+// before returning so that the executor's device buffers can be released.
+hipError_t run_grouped_gemm_once(
+    const std::vector<ProblemDesc>& problems,
+    SortMode sort_mode,
+    const KernelConfig& config,
+    hipStream_t stream = nullptr);
+
+// include/grouped_gemm/grouped_gemm.cuh:123-126
+hipError_t run_baseline_per_problem(
+    const std::vector<ProblemDesc>& problems,
+    const KernelConfig& config,
+    hipStream_t stream = nullptr);
+
+// include/grouped_gemm/grouped_gemm.cuh:128-130
+int count_non_empty_problems(
+    const std::vector<ProblemDesc>& problems,
+    const KernelConfig& config);
+
+// src/grouped_gemm.cu:912-930
+DeviceProblemDesc to_device_problem(const ProblemDesc& problem, const KernelConfig& config);
+
+// src/grouped_gemm.cu:54-65
+int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& config);
+
+// Persistent grid size build() chooses (src/grouped_gemm.cu:1228-1236):
+// config.persistent_ctas if positive, else
+// max(1, min(sm_count * max(1, active_blocks_per_sm), max(total_tiles, sm_count)));
+// 0 when total_tiles is 0.
+int grid_ctas_for(int total_tiles, const KernelConfig& config, const OccupancyInfo& occupancy);
+
+}  // namespace grouped_gemm

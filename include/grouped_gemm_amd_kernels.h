@@ -1,0 +1,170 @@
+/*
+ * grouped_gemm_amd_kernels.h -- the thin C-ABI between the C++ host runtime and
+ * the gfx950 kernels of the grouped FP16 GEMM.
+ *
+ * Everything that touches the GPU goes through these functions: device memory,
+ * kernel launches, kernel resource accounting and occupancy.  The host runtime
+ * above (include/grouped_gemm/grouped_gemm.h) is plain C++ that includes HIP's
+ * headers only for the types hipError_t, hipStream_t and __half.
+ *
+ * Plain C: POD structs, pointers and sizes, hipError_t status codes, no
+ * exceptions.  Reference counterparts are cited per entry point.
+ */
+#ifndef GROUPED_GEMM_AMD_KERNELS_H_
+#define GROUPED_GEMM_AMD_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One problem as the device reads it.  Same fields, order and meaning as
+ * DeviceProblemDesc (src/grouped_gemm.cu:25-45): the caller's ProblemDesc plus
+ * tiles_m / tiles_n, which are 0 when m <= 0 or n <= 0.  a and b point to
+ * IEEE binary16 data, row-major A[m x lda] and B[k x ldb]; c (may be NULL) and
+ * d are row-major float32 with leading dimensions ldc and ldd. */
+typedef struct gg_device_problem_desc {
+  int m;
+  int n;
+  int k;
+  const void* a;
+  const void* b;
+  const float* c;
+  float* d;
+  int lda;
+  int ldb;
+  int ldc;
+  int ldd;
+  float alpha;
+  float beta;
+  int tiles_m;
+  int tiles_n;
+} gg_device_problem_desc;
+
+/* Macro-tile shapes (src/grouped_gemm.cu:47-52). */
+enum {
+  GGK_VARIANT_64x64x16 = 0,
+  GGK_VARIANT_128x64x32 = 1,
+  GGK_VARIANT_64x128x32 = 2,
+  GGK_VARIANT_COUNT = 3
+};
+
+/* Tile compute path: FMA (the reference's SIMT path) or MFMA (the reference's
+ * tensor-core path). */
+enum { GGK_PATH_FMA = 0, GGK_PATH_MFMA = 1, GGK_PATH_COUNT = 2 };
+
+/* Kernel kinds for resource queries. */
+enum { GGK_KERNEL_GROUPED = 0, GGK_KERNEL_SINGLE = 1 };
+
+/* Ints of scheduler state one grouped launch needs (claim counter, retire
+ * counter and spares).  Must be zero before the first launch; every launch
+ * leaves it zero again when its last workgroup retires. */
+#define GGK_SCHEDULER_STATE_INTS 16
+
+typedef struct ggk_device_info {
+  int device;
+  int compute_units;
+  int max_threads_per_cu;
+  int max_wgs_per_cu;
+  int wave_size;
+  int regs_per_cu;
+  int regs_per_block;
+  int lds_per_cu;
+  int lds_per_block;
+  int l2_bytes;
+  int clock_khz;
+  int major;
+  int minor;
+  char arch_name[64];
+} ggk_device_info;
+
+/* Resources of one compiled kernel.  vgprs/agprs/sgprs/scratch come from the
+ * compiler's resource report of this build; num_regs, lds_static, local_bytes
+ * and max_threads from hipFuncGetAttributes. */
+typedef struct ggk_kernel_resources {
+  int vgprs;
+  int agprs;
+  int sgprs;
+  int scratch_bytes_per_lane;
+  int compiler_waves_per_simd;
+  int lds_bytes;
+  int num_regs;
+  int lds_static;
+  int lds_dynamic;
+  int local_bytes;
+  int max_threads;
+} ggk_kernel_resources;
+
+/* Device memory and copies (the cudaMalloc / cudaMemcpy / cudaFree calls of
+ * GroupedGemmExecutor::build and release_device_buffers,
+ * src/grouped_gemm.cu:932-948, 1178-1219). */
+hipError_t ggk_alloc(void** ptr, size_t bytes);
+hipError_t ggk_free(void* ptr);
+hipError_t ggk_copy_to_device(void* dst, const void* src, size_t bytes);
+hipError_t ggk_copy_to_host(void* dst, const void* src, size_t bytes);
+hipError_t ggk_zero(void* ptr, size_t bytes);
+hipError_t ggk_stream_synchronize(hipStream_t stream);
+hipError_t ggk_device_synchronize(void);
+
+/* Device properties of the current device (cudaGetDeviceProperties in
+ * resolve_runtime_mode and query_occupancy, src/grouped_gemm.cu:111-143,
+ * 1024-1083). */
+hipError_t ggk_device_info_get(ggk_device_info* out);
+
+/* Persistent grouped launch (launch_grouped_by_variant + grouped_gemm_kernel,
+ * src/grouped_gemm.cu:640-675, 728-751, 800-869).  d_problems[problem_count]
+ * in sorted order, d_tile_offsets[problem_count + 1], d_state holds
+ * GGK_SCHEDULER_STATE_INTS zeroed ints.  grid workgroups of 256 threads each
+ * claim tiles until total_tiles are done. */
+hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
+                              const int* d_tile_offsets, int problem_count, int total_tiles,
+                              int* d_state, int grid, hipStream_t stream);
+
+/* The same scheduler with instrumentation.  d_tile_map (may be NULL): for each
+ * claimed tile t, ints [3t, 3t+3) receive (problem, tile_m, tile_n) and no
+ * GEMM is computed.  d_wg_clock (may be NULL): for workgroup w, the
+ * 100 MHz wall clock at its start and at the end of its last tile go to
+ * [2w, 2w+2); the GEMM is computed as usual. */
+hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
+                                     const int* d_tile_offsets, int problem_count, int total_tiles,
+                                     int* d_state, int grid, int* d_tile_map, long long* d_wg_clock,
+                                     hipStream_t stream);
+
+/* One problem, one workgroup per tile, row-major tile order
+ * (single_problem_gemm_kernel + launch_single_problem_variant,
+ * src/grouped_gemm.cu:677-688, 753-769).  *problem is read on the host and
+ * passed by value; a problem with zero tiles launches nothing. */
+hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,
+                             hipStream_t stream);
+
+/* Resources of a compiled kernel (cudaFuncGetAttributes in
+ * query_occupancy_variant, src/grouped_gemm.cu:785-797). */
+hipError_t ggk_kernel_resources_get(int kernel_kind, int variant, int path, ggk_kernel_resources* out);
+
+/* Resident workgroups per CU for the grouped kernel
+ * (cudaOccupancyMaxActiveBlocksPerMultiprocessor, src/grouped_gemm.cu:778-784). */
+hipError_t ggk_occupancy(int variant, int path, int* active_wgs_per_cu);
+
+/* Fills count elements at d_dst with a counter-based hash draw from
+ * uniform[lo, hi) (fp16: rounded to nearest even; fp32: as drawn).  Element i
+ * depends only on (seed, stream_id, i).  Synthetic-input generator for tests
+ * and benchmarks. */
+hipError_t ggk_fill_uniform_f16(void* d_dst, int64_t count, uint64_t seed, uint64_t stream_id,
+                                float lo, float hi, hipStream_t stream);
+hipError_t ggk_fill_uniform_f32(float* d_dst, int64_t count, uint64_t seed, uint64_t stream_id,
+                                float lo, float hi, hipStream_t stream);
+/* Same draw mapped to a normal(0, sigma) value by Box-Muller on two hashes. */
+hipError_t ggk_fill_normal_f16(void* d_dst, int64_t count, uint64_t seed, uint64_t stream_id,
+                               float sigma, hipStream_t stream);
+/* Writes value to count floats (NaN poisoning of outputs in tests). */
+hipError_t ggk_fill_f32(float* d_dst, int64_t count, float value, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GROUPED_GEMM_AMD_KERNELS_H_ */

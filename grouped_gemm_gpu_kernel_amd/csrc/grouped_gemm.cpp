@@ -116,7 +116,7 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
   const int waves_per_simd =
       regs > 0 ? std::min(kMaxWavesPerSimd, kRegsPerLanePerSimd / round_up(regs, kRegAllocGranule))
                : kMaxWavesPerSimd;
-  info->register_limited_blocks_per_sm = std::min(info->max_blocks_per_sm, waves_per_simd);
+  info->register_limited_blocks_per_sm = waves_per_simd;
   const int lds_per_block = info->static_shared_bytes + info->dynamic_shared_bytes;
   info->lds_limited_blocks_per_sm =
       lds_per_block > 0 ? dev.lds_per_cu / lds_per_block : info->max_blocks_per_sm;

@@ -203,8 +203,11 @@ def test_grid_size_and_occupancy(torch):
             assert info.sm_count == 256 and info.using_tensor_cores == mfma
             assert info.warps_per_block == 4 and info.max_warps_per_sm == 32
             assert info.registers_per_thread > 0 and info.active_blocks_per_sm >= 1
-            assert info.active_blocks_per_sm <= min(info.register_limited_blocks_per_sm,
-                                                    info.lds_limited_blocks_per_sm)
+            # The runtime's occupancy calculator and the register/LDS accounting must agree on the
+            # binding limit.
+            assert info.active_blocks_per_sm == min(info.register_limited_blocks_per_sm,
+                                                    info.lds_limited_blocks_per_sm,
+                                                    info.wave_limited_blocks_per_sm)
             assert info.theoretical_occupancy == pytest.approx(info.active_blocks_per_sm * 4 / 32)
             for total in (1, 100, 255, 256, 257, 5000, 100000):
                 for persistent in (0, 1, 999):

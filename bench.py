@@ -39,7 +39,21 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--fma", action="store_true", help="FMA tile path instead of MFMA")
     ap.add_argument("--table", action="store_true", help="also print the reference-style results table")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB a few times (for scaling HBM "
+                         "byte counters of a profiler run) and exit")
     return ap.parse_args()
+
+
+def calibrate_copy(torch, mib: int) -> int:
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_read": n * 4, "bytes_written": n * 4, "repeats": 5}))
+    return 0
 
 
 def time_runs(torch, fn, steps: int, warmup: int) -> float:
@@ -126,6 +140,8 @@ def main() -> int:
     from grouped_gemm_gpu_kernel_amd.workloads import DeviceWorkload, make_spec
 
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        return calibrate_copy(torch, args.calibrate_copy)
     spec = make_spec(args.workload)
     config_name = args.config or spec.config
     cfg = KernelConfig.named(config_name, use_tensor_cores=not args.fma)

@@ -11,7 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgrouped_gemm_amd.so"
+LIB_PATH = Path(os.environ.get("GG_LIBRARY") or (Path(__file__).resolve().parent / "lib" / "libgrouped_gemm_amd.so"))
 
 # hipError_t values used by the API (hip_runtime_api.h).
 HIP_SUCCESS = 0
@@ -27,6 +27,7 @@ GGK_PATH_MFMA = 1
 GGK_KERNEL_GROUPED = 0
 GGK_KERNEL_SINGLE = 1
 GGK_SCHEDULER_STATE_INTS = 16
+GGK_SCHEDULER_CHUNKS = 8
 
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_ll_p = ctypes.POINTER(ctypes.c_longlong)
@@ -119,8 +120,8 @@ SIGNATURES = {
     "ggk_stream_synchronize": (_i, [_vp]),
     "ggk_device_synchronize": (_i, []),
     "ggk_device_info_get": (_i, [_P(GGKDeviceInfo)]),
-    "ggk_launch_grouped": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, _i, _vp]),
-    "ggk_launch_grouped_traced": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _vp]),
+    "ggk_launch_grouped": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
+    "ggk_launch_grouped_traced": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp, _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
     "ggk_kernel_resources_get": (_i, [_i, _i, _i, _P(GGKKernelResources)]),
     "ggk_occupancy": (_i, [_i, _i, c_int_p]),

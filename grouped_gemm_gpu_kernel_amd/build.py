@@ -83,17 +83,23 @@ def parse_resource_report(report: str) -> list[tuple[int, ...]]:
     return rows
 
 
-def build_library() -> Path:
-    BUILD.mkdir(parents=True, exist_ok=True)
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    kernels_o = BUILD / "gg_kernels.o"
+def build_library(out_path: Path | None = None, defines: tuple[str, ...] = ()) -> Path:
+    """Builds the shared library (default: lib/libgrouped_gemm_amd.so).  `defines`
+    adds -D options to the kernel compile (tuning experiments build variants
+    into other paths)."""
+    out = Path(out_path) if out_path else LIB_DIR / LIB_NAME
+    build_dir = BUILD if out_path is None else out.parent / ("_build_" + out.stem)
+    build_dir.mkdir(parents=True, exist_ok=True)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    kernels_o = build_dir / "gg_kernels.o"
+    extra = [f"-D{d}" for d in defines]
 
     def compile_kernels() -> str:
-        return _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c",
+        return _run([HIPCC, *HIP_FLAGS, *extra, "-Rpass-analysis=kernel-resource-usage", "-c",
                      str(CSRC / "gg_kernels.hip"), "-o", str(kernels_o)], capture_stderr=True)
 
     def compile_host(name: str) -> Path:
-        obj = BUILD / (Path(name).stem + ".o")
+        obj = build_dir / (Path(name).stem + ".o")
         _run([*CXX_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
         return obj
 
@@ -106,12 +112,11 @@ def build_library() -> Path:
     if len(rows) != 12:
         raise RuntimeError(f"expected 12 kernel resource rows, parsed {len(rows)}")
     table = "".join("    {%d, %d, %d, %d, %d, %d, %d, %d, %d},\n" % r for r in sorted(rows))
-    (BUILD / "gg_resources_table.inc").write_text(table)
-    res_o = BUILD / "gg_resources.o"
-    _run([*CXX_FLAGS, f"-I{BUILD}", "-c", str(CSRC / "gg_resources.cpp"), "-o", str(res_o)])
+    (build_dir / "gg_resources_table.inc").write_text(table)
+    res_o = build_dir / "gg_resources.o"
+    _run([*CXX_FLAGS, f"-I{build_dir}", "-c", str(CSRC / "gg_resources.cpp"), "-o", str(res_o)])
 
-    out = LIB_DIR / LIB_NAME
-    tmp = LIB_DIR / (LIB_NAME + ".tmp")
+    tmp = out.parent / (out.name + ".tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(kernels_o),
           *map(str, host_objs), str(res_o)])
     os.replace(tmp, out)

@@ -42,15 +42,35 @@ __device__ __forceinline__ gg_device_problem_desc load_problem(const gg_device_p
   return __builtin_bit_cast(gg_device_problem_desc, words);
 }
 
+constexpr int kChunks = GGK_SCHEDULER_CHUNKS;  // one per XCD
+
 struct GroupedArgs {
   const gg_device_problem_desc* __restrict__ problems;
   const int* __restrict__ offsets;
   int count;
   int total;
-  int* state;          // [0] claim counter, [1] retired workgroups
+  int* state;          // [0, kChunks) chunk claim counters, [kChunks] retired workgroups
   int* tile_map;       // traced launches only
   long long* wg_clock; // traced launches only
+  int bounds[kChunks + 1];  // chunk c owns tile indices [bounds[c], bounds[c + 1])
 };
+
+// Claims the next tile index for the calling workgroup (one thread calls it).
+// Workgroups are dispatched to the XCDs round-robin, so workgroup w runs on
+// XCD w % kChunks and starts on that chunk: the tiles of one problem, which
+// share A and B panels, are then multiplied on one XCD and its L2 serves the
+// re-reads.  When a chunk runs dry the workgroup moves on to the next one
+// (stealing); `visit` counts the chunks it has left behind.  Returns total
+// when every chunk is exhausted.
+__device__ __forceinline__ int claim_tile(const GroupedArgs& args, int home, int& visit) {
+  while (visit < kChunks) {
+    const int c = (home + visit) % kChunks;
+    const int t = args.bounds[c] + atomicAdd(args.state + c, 1);
+    if (t < args.bounds[c + 1]) return t;
+    ++visit;
+  }
+  return args.total;
+}
 
 // Index of the problem that owns tile t: the number of problems p with
 // offsets[p + 1] <= t, i.e. upper_bound over offsets[1..count] -- the same
@@ -96,13 +116,15 @@ __global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) 
     clock_end = clock_start;
   }
 
+  const int home = blockIdx.x % kChunks;
+  int visit = 0;  // meaningful in thread 0 only
   int next = 0;
-  if (tid == 0) s_claim = atomicAdd(args.state, 1);
+  if (tid == 0) s_claim = claim_tile(args, home, visit);
   __syncthreads();
   int t = __builtin_amdgcn_readfirstlane(s_claim);
   while (t < args.total) {
     // Claim the next index now; its latency hides behind this tile's work.
-    if (tid == 0) next = atomicAdd(args.state, 1);
+    if (tid == 0) next = claim_tile(args, home, visit);
 
     const int prob = find_problem(args.offsets, args.count, t);
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
@@ -136,13 +158,12 @@ __global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) 
       args.wg_clock[2 * blockIdx.x + 0] = clock_start;
       args.wg_clock[2 * blockIdx.x + 1] = clock_end;
     }
-    // Every workgroup makes exactly one claim past the end before it retires,
-    // so the last one to retire knows no claim is still in flight and returns
-    // the state to zero for the next launch in stream order.
-    const int retired = atomicAdd(args.state + 1, 1);
+    // A workgroup retires only after a failed claim on every chunk, so when
+    // the last one retires no claim is in flight: it returns the counters to
+    // zero for the next launch in stream order.
+    const int retired = atomicAdd(args.state + kChunks, 1);
     if (retired == (int)gridDim.x - 1) {
-      atomicExch(args.state + 0, 0);
-      atomicExch(args.state + 1, 0);
+      for (int c = 0; c <= kChunks; ++c) atomicExch(args.state + c, 0);
     }
   }
 }
@@ -312,9 +333,25 @@ hipError_t ggk_device_info_get(ggk_device_info* out) {
   return hipSuccess;
 }
 
+static void fill_bounds(GroupedArgs& args, const int* chunk_bounds) {
+  for (int c = 0; c <= kChunks; ++c) {
+    args.bounds[c] = chunk_bounds != nullptr ? chunk_bounds[c]
+                                             : (int)((int64_t)args.total * c / kChunks);
+  }
+}
+
+static bool bounds_valid(const int* chunk_bounds, int total_tiles) {
+  if (chunk_bounds == nullptr) return true;
+  if (chunk_bounds[0] != 0 || chunk_bounds[kChunks] != total_tiles) return false;
+  for (int c = 0; c < kChunks; ++c) {
+    if (chunk_bounds[c + 1] < chunk_bounds[c]) return false;
+  }
+  return true;
+}
+
 hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
                               const int* d_tile_offsets, int problem_count, int total_tiles,
-                              int* d_state, int grid, hipStream_t stream) {
+                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream) {
   if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
     return hipErrorInvalidValue;
   }
@@ -322,7 +359,9 @@ hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_des
   if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, nullptr, nullptr};
+  if (!bounds_valid(chunk_bounds, total_tiles)) return hipErrorInvalidValue;
+  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, nullptr, nullptr, {}};
+  fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
   return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].grouped), dim3(grid),
                          dim3(kThreads), params, 0, stream);
@@ -330,8 +369,8 @@ hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_des
 
 hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
                                      const int* d_tile_offsets, int problem_count, int total_tiles,
-                                     int* d_state, int grid, int* d_tile_map, long long* d_wg_clock,
-                                     hipStream_t stream) {
+                                     int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
+                                     long long* d_wg_clock, hipStream_t stream) {
   if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
     return hipErrorInvalidValue;
   }
@@ -339,7 +378,9 @@ hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_prob
   if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, d_tile_map, d_wg_clock};
+  if (!bounds_valid(chunk_bounds, total_tiles)) return hipErrorInvalidValue;
+  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, d_tile_map, d_wg_clock, {}};
+  fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
   return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].traced), dim3(grid),
                          dim3(kThreads), params, 0, stream);

@@ -12,6 +12,42 @@
 
 namespace gg {
 
+// Runs the staged k-loop of one tile: compute(stage_pointer) is called once
+// per stage with that stage's LDS buffer.
+//
+// Stage s is fetched into register set s % DEPTH.  While stage k is
+// multiplied out of LDS buffer k % 2, the loads of stage k + DEPTH - 1 are
+// issued and stage k + 1 (issued DEPTH - 1 stages earlier) is written to the
+// other LDS buffer; one barrier closes the step.  The loop body is unrolled
+// DEPTH times so that every register set is addressed statically.
+template <class G, class Compute>
+__device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
+                                           Compute&& compute) {
+  constexpr int D = G::DEPTH;
+  const int nk = (p.k + G::BK - 1) / G::BK;
+  if (nk <= 0) return;
+  const StageLoader<G> loader(p, m0, n0);
+  RawStage<G> ring[D];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) {
+    if (s < nk) loader.issue(s, ring[s]);
+  }
+  loader.store(ring[0], 0, lds, 0);
+  __syncthreads();
+  for (int k0 = 0; k0 < nk; k0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int k = k0 + u;
+      if (k < nk) {
+        if (k + D - 1 < nk) loader.issue(k + D - 1, ring[(u + D - 1) % D]);
+        compute(lds + (k & 1) * G::STAGE);
+        if (k + 1 < nk) loader.store(ring[(u + 1) % D], k + 1, lds, (k + 1) & 1);
+        __syncthreads();
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // MFMA tile: v_mfma_f32_32x32x16_f16, 4 waves in a 2 x 2 grid, each wave owns a
 // (BM/2) x (BN/2) block of D held as (BM/64) x (BN/64) 32x32 accumulators.
@@ -58,7 +94,8 @@ struct MfmaTile {
       for (int fn = 0; fn < FN; ++fn) {
         const int nb = wn * WN + fn * 32 + 16 * (g & 1);
         const int kb = s * 16 + 8 * (g >> 1);
-        const uint16_t* src = bs + (kb + (j >> 2)) * G::SB + nb + 4 * (j & 3);
+        // Rows kb + j/4 and kb + 4 + j/4 share one swizzle (it depends on k mod 4).
+        const uint16_t* src = bs + G::b_chunk(kb + (j >> 2), nb + 4 * (j & 3));
         const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GG_LDS short4_t*)(src));
         const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GG_LDS short4_t*)(src + 4 * G::SB));
         bf[fn] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -82,9 +119,6 @@ struct MfmaTile {
     const int wn = wave & 1;
     const int m0 = tile_m * G::BM;
     const int n0 = tile_n * G::BN;
-    // A wave whose block starts past the problem's edge multiplies zeros and
-    // stores nothing.
-    const bool active = (m0 + wm * WM < p.m) && (n0 + wn * WN < p.n);
 
     floatx16_t acc[FM][FN];
 #pragma unroll
@@ -94,22 +128,11 @@ struct MfmaTile {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[fm][fn][e] = 0.0f;
 
-    const int nk = (p.k + G::BK - 1) / G::BK;
-    if (nk > 0) {
-      StageRegs<G> regs;
-      load_stage<G>(p, m0, n0, 0, regs);
-      store_stage<G>(lds, 0, regs);
-      __syncthreads();
-      for (int kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        if (more) load_stage<G>(p, m0, n0, kt + 1, regs);
-        compute_stage(lds + (kt & 1) * G::STAGE, lane, wm, wn, acc);
-        if (more) store_stage<G>(lds, (kt + 1) & 1, regs);
-        __syncthreads();
-      }
-    }
+    run_k_loop<G>(p, m0, n0, lds, [&](const uint16_t* stage) { compute_stage(stage, lane, wm, wn, acc); });
 
-    if (!active) return;
+    // A wave whose block starts past the problem's edge multiplied zeros and
+    // stores nothing.
+    if (m0 + wm * WM >= p.m || n0 + wn * WN >= p.n) return;
     const bool use_c = p.c != nullptr && p.beta != 0.0f;
     g_cf32_t* cptr = (g_cf32_t*)p.c;
     g_f32_t* dptr = (g_f32_t*)p.d;
@@ -150,7 +173,7 @@ template <class G>
 struct FmaTile {
   static constexpr int RM = G::BM / 16;
   static constexpr int RN = G::BN / 16;
-  static_assert(RN == 4 || RN == 8, "column block must be one 8- or 16-byte LDS read");
+  static_assert(RN == 4 || RN == 8, "column block must be one or two LDS chunks");
 
   __device__ __forceinline__ static void compute_stage(const uint16_t* stage, int krem, int tm, int tn,
                                                        float (&acc)[RM][RN]) {
@@ -166,7 +189,7 @@ struct FmaTile {
       }
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const uint16_t* brow = bs + (k8 * 8 + kk) * G::SB + tn * RN;
+        const uint16_t* brow = bs + G::b_chunk(k8 * 8 + kk, tn * RN);
         float bv[RN];
         if constexpr (RN == 4) {
           const half4_t h = *reinterpret_cast<const half4_t*>(brow);
@@ -203,20 +226,11 @@ struct FmaTile {
 #pragma unroll
       for (int j = 0; j < RN; ++j) acc[i][j] = 0.0f;
 
-    const int nk = (p.k + G::BK - 1) / G::BK;
-    if (nk > 0) {
-      StageRegs<G> regs;
-      load_stage<G>(p, m0, n0, 0, regs);
-      store_stage<G>(lds, 0, regs);
-      __syncthreads();
-      for (int kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        if (more) load_stage<G>(p, m0, n0, kt + 1, regs);
-        if (active) compute_stage(lds + (kt & 1) * G::STAGE, p.k - kt * G::BK, tm, tn, acc);
-        if (more) store_stage<G>(lds, (kt + 1) & 1, regs);
-        __syncthreads();
-      }
-    }
+    int kt = 0;
+    run_k_loop<G>(p, m0, n0, lds, [&](const uint16_t* stage) {
+      if (active) compute_stage(stage, p.k - kt * G::BK, tm, tn, acc);
+      ++kt;
+    });
 
     if (!active) return;
     const bool use_c = p.c != nullptr && p.beta != 0.0f;

@@ -7,6 +7,7 @@
 #include "grouped_gemm/grouped_gemm.h"
 
 #include <algorithm>
+#include <array>
 #include <cstring>
 #include <numeric>
 #include <tuple>
@@ -129,6 +130,45 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
         static_cast<float>(info->active_warps_per_sm) / static_cast<float>(info->max_warps_per_sm);
   }
   return hipSuccess;
+}
+
+// Splits the tile indices [0, total) into GGK_SCHEDULER_CHUNKS contiguous
+// chunks of about equal memory cost, one per XCD.  A tile of problem p moves
+// (BM + BN) * k binary16 values in and BM * BN floats out (twice when C is
+// read); the grouped kernel on these shapes is bound by those bytes.
+std::array<int, GGK_SCHEDULER_CHUNKS + 1> plan_chunks(const std::vector<DeviceProblemDesc>& problems,
+                                                      const std::vector<int>& offsets,
+                                                      const KernelConfig& config) {
+  constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
+  std::array<int, kChunks + 1> bounds{};
+  const int total = offsets.back();
+  std::vector<double> cost(problems.size());
+  double sum = 0.0;
+  for (size_t i = 0; i < problems.size(); ++i) {
+    const DeviceProblemDesc& p = problems[i];
+    const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+    cost[i] = 2.0 * (config.cta_m + config.cta_n) * std::max(p.k, 0) +
+              4.0 * config.cta_m * config.cta_n * (reads_c ? 2.0 : 1.0);
+    sum += cost[i] * (offsets[i + 1] - offsets[i]);
+  }
+  bounds[0] = 0;
+  bounds[kChunks] = total;
+  double before = 0.0;  // cost of all tiles of problems before i
+  size_t i = 0;
+  for (int c = 1; c < kChunks; ++c) {
+    const double target = sum * c / kChunks;
+    while (i < problems.size() && before + cost[i] * (offsets[i + 1] - offsets[i]) < target) {
+      before += cost[i] * (offsets[i + 1] - offsets[i]);
+      ++i;
+    }
+    int t = total;
+    if (i < problems.size()) {
+      const int into = cost[i] > 0.0 ? static_cast<int>((target - before) / cost[i]) : 0;
+      t = std::min(offsets[i] + into, offsets[i + 1]);
+    }
+    bounds[c] = std::max(bounds[c - 1], std::min(t, total));
+  }
+  return bounds;
 }
 
 void release(DeviceProblemDesc*& problems, int*& offsets, int*& state) {
@@ -264,6 +304,7 @@ struct GroupedGemmExecutor::Impl {
   KernelConfig config{};
   int variant = -1;
   int path = GGK_PATH_FMA;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> chunk_bounds{};
 };
 
 GroupedGemmExecutor::GroupedGemmExecutor() : impl_(new Impl()) {}
@@ -349,6 +390,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (status != hipSuccess) return status;
   }
 
+  impl_->chunk_bounds = plan_chunks(device_problems, prepared.tile_offsets, config);
+
   OccupancyInfo occupancy{};
   status = fill_occupancy(config, mode, &occupancy);
   if (status != hipSuccess) return status;
@@ -363,7 +406,8 @@ hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
-                            impl_->problem_count, impl_->total_tiles, impl_->d_state, impl_->grid_ctas, stream);
+                            impl_->problem_count, impl_->total_tiles, impl_->d_state,
+                            impl_->chunk_bounds.data(), impl_->grid_ctas, stream);
 }
 
 hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
@@ -371,7 +415,8 @@ hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_cloc
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
                                    impl_->problem_count, impl_->total_tiles, impl_->d_state,
-                                   impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
+                                   impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map, d_wg_clock,
+                                   stream);
 }
 
 int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }

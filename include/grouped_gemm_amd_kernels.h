@@ -60,9 +60,15 @@ enum { GGK_PATH_FMA = 0, GGK_PATH_MFMA = 1, GGK_PATH_COUNT = 2 };
 /* Kernel kinds for resource queries. */
 enum { GGK_KERNEL_GROUPED = 0, GGK_KERNEL_SINGLE = 1 };
 
-/* Ints of scheduler state one grouped launch needs (claim counter, retire
- * counter and spares).  Must be zero before the first launch; every launch
- * leaves it zero again when its last workgroup retires. */
+/* The persistent grid claims tiles from GGK_SCHEDULER_CHUNKS contiguous
+ * chunks of the tile index range, one per XCD (an MI355X has 8); workgroup w
+ * starts on chunk w % GGK_SCHEDULER_CHUNKS and moves to the next chunk when
+ * its own is exhausted. */
+#define GGK_SCHEDULER_CHUNKS 8
+
+/* Ints of scheduler state one grouped launch needs: a claim counter per chunk,
+ * a retire counter, spares.  Must be zero before the first launch; every
+ * launch leaves it zero again when its last workgroup retires. */
 #define GGK_SCHEDULER_STATE_INTS 16
 
 typedef struct ggk_device_info {
@@ -118,11 +124,13 @@ hipError_t ggk_device_info_get(ggk_device_info* out);
 /* Persistent grouped launch (launch_grouped_by_variant + grouped_gemm_kernel,
  * src/grouped_gemm.cu:640-675, 728-751, 800-869).  d_problems[problem_count]
  * in sorted order, d_tile_offsets[problem_count + 1], d_state holds
- * GGK_SCHEDULER_STATE_INTS zeroed ints.  grid workgroups of 256 threads each
- * claim tiles until total_tiles are done. */
+ * GGK_SCHEDULER_STATE_INTS zeroed ints.  chunk_bounds (host memory,
+ * GGK_SCHEDULER_CHUNKS + 1 non-decreasing ints from 0 to total_tiles, or NULL
+ * for equal tile counts) splits the tile indices into the per-XCD chunks.
+ * grid workgroups of 256 threads each claim tiles until total_tiles are done. */
 hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
                               const int* d_tile_offsets, int problem_count, int total_tiles,
-                              int* d_state, int grid, hipStream_t stream);
+                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream);
 
 /* The same scheduler with instrumentation.  d_tile_map (may be NULL): for each
  * claimed tile t, ints [3t, 3t+3) receive (problem, tile_m, tile_n) and no
@@ -131,8 +139,8 @@ hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_des
  * [2w, 2w+2); the GEMM is computed as usual. */
 hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
                                      const int* d_tile_offsets, int problem_count, int total_tiles,
-                                     int* d_state, int grid, int* d_tile_map, long long* d_wg_clock,
-                                     hipStream_t stream);
+                                     int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
+                                     long long* d_wg_clock, hipStream_t stream);
 
 /* One problem, one workgroup per tile, row-major tile order
  * (single_problem_gemm_kernel + launch_single_problem_variant,

@@ -26,6 +26,8 @@ GGK_PATH_FMA = 0
 GGK_PATH_MFMA = 1
 GGK_KERNEL_GROUPED = 0
 GGK_KERNEL_SINGLE = 1
+GGK_ADDR_32 = 0
+GGK_ADDR_64 = 1
 GGK_SCHEDULER_STATE_INTS = 16
 GGK_SCHEDULER_CHUNKS = 8
 
@@ -84,6 +86,10 @@ class GGKKernelResources(ctypes.Structure):
         "num_regs", "lds_static", "lds_dynamic", "local_bytes", "max_threads")]
 
 
+class GGKWorkShape(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int) for name in ("tiles_m", "tiles_n", "threads", "rows", "stage_k")]
+
+
 _P = ctypes.POINTER
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -120,8 +126,10 @@ SIGNATURES = {
     "ggk_stream_synchronize": (_i, [_vp]),
     "ggk_device_synchronize": (_i, []),
     "ggk_device_info_get": (_i, [_P(GGKDeviceInfo)]),
-    "ggk_launch_grouped": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
-    "ggk_launch_grouped_traced": (_i, [_i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp, _vp]),
+    "ggk_work_shape_get": (_i, [_i, _i, _P(GGKWorkShape)]),
+    "ggk_needs_addr64": (_i, [_i, _i, _P(GGDeviceProblemDesc)]),
+    "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
+    "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp, _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
     "ggk_kernel_resources_get": (_i, [_i, _i, _i, _P(GGKKernelResources)]),
     "ggk_occupancy": (_i, [_i, _i, c_int_p]),

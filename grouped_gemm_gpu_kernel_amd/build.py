@@ -22,7 +22,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-CSRC = PKG / "csrc"
+CSRC_DIR = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libgrouped_gemm_amd.so"
@@ -34,7 +34,7 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # Packed FP32 instructions stay off (they have given wrong results on these GPUs).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+    f"-I{ROOT / 'include'}", f"-I{CSRC_DIR}",
 ]
 CXX_FLAGS = [
     "g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
@@ -43,7 +43,8 @@ CXX_FLAGS = [
 
 _REMARK = re.compile(r"remark:\s+(Function Name|TotalSGPRs|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
                      r"Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]):\s+(\S+)")
-_KERNEL = re.compile(r"gg_(grouped|single)_kernelILi(\d+)ELi(\d+)E(Lb([01])E)?")
+# gg_grouped_kernel<variant, path, traced, wide> and gg_single_kernel<variant, path, wide>.
+_KERNEL = re.compile(r"gg_(grouped|single)_kernelILi(\d+)ELi(\d+)ELb([01])E(Lb([01])E)?")
 
 
 def _run(cmd: list[str], capture_stderr: bool = False) -> str:
@@ -56,7 +57,8 @@ def _run(cmd: list[str], capture_stderr: bool = False) -> str:
 
 def parse_resource_report(report: str) -> list[tuple[int, ...]]:
     """Rows (kind, variant, path, vgprs, agprs, sgprs, scratch, waves, lds) for
-    the untraced grouped kernels and the single-problem kernels."""
+    the untraced grouped kernels and the single-problem kernels in the 32-bit
+    addressing form."""
     rows, cur = [], {}
 
     def flush():
@@ -64,8 +66,10 @@ def parse_resource_report(report: str) -> list[tuple[int, ...]]:
         if not m:
             return
         kind = 0 if m.group(1) == "grouped" else 1
-        if kind == 0 and m.group(5) != "0":
-            return  # traced instantiation: same code plus instrumentation
+        if kind == 0 and (m.group(4) != "0" or m.group(6) != "0"):
+            return  # traced (same code plus instrumentation) or 64-bit addressing form
+        if kind == 1 and m.group(4) != "0":
+            return  # 64-bit addressing form
         rows.append((kind, int(m.group(2)), int(m.group(3)), int(cur.get("VGPRs", 0)),
                      int(cur.get("AGPRs", 0)), int(cur.get("TotalSGPRs", 0)),
                      int(cur.get("ScratchSize [bytes/lane]", 0)),
@@ -83,10 +87,11 @@ def parse_resource_report(report: str) -> list[tuple[int, ...]]:
     return rows
 
 
-def build_library(out_path: Path | None = None, defines: tuple[str, ...] = ()) -> Path:
+def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), csrc: Path | None = None) -> Path:
     """Builds the shared library (default: lib/libgrouped_gemm_amd.so).  `defines`
-    adds -D options to the kernel compile (tuning experiments build variants
-    into other paths)."""
+    adds -D options to the kernel compile and `csrc` replaces the source folder
+    (tuning experiments build variants into other paths)."""
+    CSRC = Path(csrc) if csrc is not None else CSRC_DIR
     out = Path(out_path) if out_path else LIB_DIR / LIB_NAME
     build_dir = BUILD if out_path is None else out.parent / ("_build_" + out.stem)
     build_dir.mkdir(parents=True, exist_ok=True)
@@ -100,7 +105,7 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = ()) -
 
     def compile_host(name: str) -> Path:
         obj = build_dir / (Path(name).stem + ".o")
-        _run([*CXX_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
+        _run([*CXX_FLAGS, f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)])
         return obj
 
     with ThreadPoolExecutor(max_workers=3) as pool:

@@ -4,10 +4,13 @@
 // Kernels:
 //   gg_grouped_kernel  persistent scheduler (grouped_gemm_kernel,
 //                      src/grouped_gemm.cu:640-675): one launch, workgroups
-//                      claim tile indices from a device-wide counter until all
-//                      total_tiles are taken; each index is mapped to
-//                      (problem, tile_m, tile_n) by a search over tile_offsets.
-//   gg_single_kernel   one problem, one workgroup per tile
+//                      claim work-tile indices from device-wide counters until
+//                      all are taken; each index is mapped to (problem, work
+//                      tile) by a search over the work-tile offsets.  A work
+//                      tile is a TM x TN block of the reference's macro-tiles
+//                      (KernelShape), so every reference tile index t maps to
+//                      the same (problem, tile_m, tile_n) as in the reference.
+//   gg_single_kernel   one problem, one workgroup per work tile
 //                      (single_problem_gemm_kernel, src/grouped_gemm.cu:677-688).
 //   fill kernels       synthetic inputs and output poisoning for tests/benches.
 #include <hip/hip_runtime.h>
@@ -46,16 +49,17 @@ constexpr int kChunks = GGK_SCHEDULER_CHUNKS;  // one per XCD
 
 struct GroupedArgs {
   const gg_device_problem_desc* __restrict__ problems;
-  const int* __restrict__ offsets;
+  const int* __restrict__ tile_offsets;  // reference tiles: [count + 1]
+  const int* __restrict__ work_offsets;  // work tiles: [count + 1]
   int count;
-  int total;
+  int total;           // work tiles
   int* state;          // [0, kChunks) chunk claim counters, [kChunks] retired workgroups
   int* tile_map;       // traced launches only
   long long* wg_clock; // traced launches only
-  int bounds[kChunks + 1];  // chunk c owns tile indices [bounds[c], bounds[c + 1])
+  int bounds[kChunks + 1];  // chunk c owns work-tile indices [bounds[c], bounds[c + 1])
 };
 
-// Claims the next tile index for the calling workgroup (one thread calls it).
+// Claims the next work-tile index for the calling workgroup (one thread calls it).
 // Workgroups are dispatched to the XCDs round-robin, so workgroup w runs on
 // XCD w % kChunks and starts on that chunk: the tiles of one problem, which
 // share A and B panels, are then multiplied on one XCD and its L2 serves the
@@ -72,10 +76,10 @@ __device__ __forceinline__ int claim_tile(const GroupedArgs& args, int home, int
   return args.total;
 }
 
-// Index of the problem that owns tile t: the number of problems p with
+// Index of the problem that owns index t: the number of problems p with
 // offsets[p + 1] <= t, i.e. upper_bound over offsets[1..count] -- the same
-// function as find_problem_by_tile (src/grouped_gemm.cu:219-234).  Problems
-// with zero tiles never own an index.
+// function as find_problem_by_tile (src/grouped_gemm.cu:219-234), here over
+// the work-tile offsets.  Problems with zero tiles never own an index.
 //
 // Evaluated by the whole wave at once: each step tests 64 evenly spaced
 // candidates in parallel and keeps the span between the last true and the
@@ -101,9 +105,21 @@ __device__ __forceinline__ int find_problem(const int* __restrict__ offsets, int
   return __builtin_amdgcn_readfirstlane(lo + __popcll(__ballot(below)));
 }
 
-template <int V, int PATH, bool TRACED>
-__global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) {
-  using G = typename VariantGeometry<V>::type;
+// Work tiles of a problem along M and N.
+template <int TM, int TN>
+__device__ __forceinline__ int work_tiles_n(const gg_device_problem_desc& p) {
+  return (p.tiles_n + TN - 1) / TN;
+}
+
+// At most 256 VGPRs + AGPRs per lane: two waves per SIMD (a 512-thread
+// workgroup, or two 256-thread ones).
+#define GG_KERNEL_ATTRS(V, PATH) \
+  __launch_bounds__((KernelShape<V, PATH>::G::THREADS)) __attribute__((amdgpu_waves_per_eu(2)))
+
+template <int V, int PATH, bool TRACED, bool WIDE>
+__global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
+  using S = KernelShape<V, PATH>;
+  using G = typename S::G;
   using Tile = typename TileFor<PATH, G>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
   __shared__ int s_claim;
@@ -126,22 +142,31 @@ __global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) 
     // Claim the next index now; its latency hides behind this tile's work.
     if (tid == 0) next = claim_tile(args, home, visit);
 
-    const int prob = find_problem(args.offsets, args.count, t);
+    const int prob = find_problem(args.work_offsets, args.count, t);
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
     const gg_device_problem_desc p = load_problem(args.problems, prob);
-    const int local = t - ((const_int_ptr)args.offsets)[prob];
-    if (p.tiles_n > 0) {
-      const int tile_m = local / p.tiles_n;
-      const int tile_n = local - tile_m * p.tiles_n;
-      if (tile_m < p.tiles_m) {
+    const int local = t - ((const_int_ptr)args.work_offsets)[prob];
+    const int wtn = work_tiles_n<S::TM, S::TN>(p);
+    if (wtn > 0) {
+      const int wm = local / wtn;
+      const int wn = local - wm * wtn;
+      if (wm * S::TM < p.tiles_m) {
         if (TRACED && args.tile_map != nullptr) {
-          if (tid == 0) {
-            args.tile_map[3 * t + 0] = prob;
-            args.tile_map[3 * t + 1] = tile_m;
-            args.tile_map[3 * t + 2] = tile_n;
+          // Record every reference tile this work tile covers under its
+          // reference index.
+          const int base = ((const_int_ptr)args.tile_offsets)[prob];
+          if (tid < S::TM * S::TN) {
+            const int tm = wm * S::TM + tid / S::TN;
+            const int tn = wn * S::TN + tid % S::TN;
+            if (tm < p.tiles_m && tn < p.tiles_n) {
+              const int ref = base + tm * p.tiles_n + tn;
+              args.tile_map[3 * ref + 0] = prob;
+              args.tile_map[3 * ref + 1] = tm;
+              args.tile_map[3 * ref + 2] = tn;
+            }
           }
         } else {
-          Tile::run(p, tile_m, tile_n, lds);
+          Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds);
         }
       }
     }
@@ -168,16 +193,19 @@ __global__ __launch_bounds__(kThreads) void gg_grouped_kernel(GroupedArgs args) 
   }
 }
 
-template <int V, int PATH>
-__global__ __launch_bounds__(kThreads) void gg_single_kernel(gg_device_problem_desc p) {
-  using G = typename VariantGeometry<V>::type;
+template <int V, int PATH, bool WIDE>
+__global__ GG_KERNEL_ATTRS(V, PATH) void gg_single_kernel(gg_device_problem_desc p) {
+  using S = KernelShape<V, PATH>;
+  using G = typename S::G;
   using Tile = typename TileFor<PATH, G>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
   const int t = blockIdx.x;
-  if (p.tiles_n <= 0 || t >= p.tiles_m * p.tiles_n) return;
-  const int tile_m = t / p.tiles_n;
-  const int tile_n = t - tile_m * p.tiles_n;
-  Tile::run(p, tile_m, tile_n, lds);
+  const int wtn = work_tiles_n<S::TM, S::TN>(p);
+  const int wtm = (p.tiles_m + S::TM - 1) / S::TM;
+  if (wtn <= 0 || t >= wtm * wtn) return;
+  const int wm = t / wtn;
+  const int wn = t - wm * wtn;
+  Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -237,26 +265,38 @@ __global__ void fill_f32_kernel(float* dst, int64_t count, float value) {
 using GroupedFn = void (*)(GroupedArgs);
 using SingleFn = void (*)(gg_device_problem_desc);
 
+// Index [0] of each kernel array is the 32-bit-offset form, [1] the WIDE form.
 template <int V, int P>
 struct KernelEntry {
-  static constexpr GroupedFn grouped = gg_grouped_kernel<V, P, false>;
-  static constexpr GroupedFn traced = gg_grouped_kernel<V, P, true>;
-  static constexpr SingleFn single = gg_single_kernel<V, P>;
+  static constexpr int threads = KernelShape<V, P>::G::THREADS;
+  static constexpr int tm = KernelShape<V, P>::TM;
+  static constexpr int tn = KernelShape<V, P>::TN;
+  static constexpr int bm = KernelShape<V, P>::G::BM;
+  static constexpr int bk = KernelShape<V, P>::G::BK;
 };
 
-#define GG_ROW(V) \
-  {{KernelEntry<V, 0>::grouped, KernelEntry<V, 0>::traced, KernelEntry<V, 0>::single}, \
-   {KernelEntry<V, 1>::grouped, KernelEntry<V, 1>::traced, KernelEntry<V, 1>::single}}
+#define GG_ENTRY(V, P)                                                                               \
+  {{gg_grouped_kernel<V, P, false, false>, gg_grouped_kernel<V, P, false, true>},                   \
+   {gg_grouped_kernel<V, P, true, false>, gg_grouped_kernel<V, P, true, true>},                     \
+   {gg_single_kernel<V, P, false>, gg_single_kernel<V, P, true>}, KernelEntry<V, P>::threads,        \
+   KernelEntry<V, P>::tm, KernelEntry<V, P>::tn, KernelEntry<V, P>::bm, KernelEntry<V, P>::bk}
+#define GG_ROW(V) {GG_ENTRY(V, 0), GG_ENTRY(V, 1)}
 
 struct KernelSet {
-  GroupedFn grouped;
-  GroupedFn traced;
-  SingleFn single;
+  GroupedFn grouped[2];
+  GroupedFn traced[2];
+  SingleFn single[2];
+  int threads;
+  int tm;
+  int tn;
+  int bm;  // work-tile rows
+  int bk;  // stage depth
 };
 
 static const KernelSet kKernels[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {
     GG_ROW(GGK_VARIANT_64x64x16), GG_ROW(GGK_VARIANT_128x64x32), GG_ROW(GGK_VARIANT_64x128x32)};
 #undef GG_ROW
+#undef GG_ENTRY
 
 static bool valid_kernel(int variant, int path) {
   return variant >= 0 && variant < GGK_VARIANT_COUNT && path >= 0 && path < GGK_PATH_COUNT;
@@ -340,62 +380,96 @@ static void fill_bounds(GroupedArgs& args, const int* chunk_bounds) {
   }
 }
 
-static bool bounds_valid(const int* chunk_bounds, int total_tiles) {
+static bool bounds_valid(const int* chunk_bounds, int total) {
   if (chunk_bounds == nullptr) return true;
-  if (chunk_bounds[0] != 0 || chunk_bounds[kChunks] != total_tiles) return false;
+  if (chunk_bounds[0] != 0 || chunk_bounds[kChunks] != total) return false;
   for (int c = 0; c < kChunks; ++c) {
     if (chunk_bounds[c + 1] < chunk_bounds[c]) return false;
   }
   return true;
 }
 
-hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
-                              const int* d_tile_offsets, int problem_count, int total_tiles,
-                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream) {
-  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
+static hipError_t launch_grouped(int variant, int path, int addressing, bool traced,
+                                 const gg_device_problem_desc* d_problems,
+                                 const int* d_tile_offsets, const int* d_work_offsets, int problem_count,
+                                 int total_work, int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
+                                 long long* d_wg_clock, hipStream_t stream) {
+  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_work < 0 ||
+      (addressing != GGK_ADDR_32 && addressing != GGK_ADDR_64)) {
     return hipErrorInvalidValue;
   }
-  if (total_tiles == 0 || problem_count == 0) return hipSuccess;
-  if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
+  if (total_work == 0 || problem_count == 0) return hipSuccess;
+  if (d_problems == nullptr || d_work_offsets == nullptr || d_state == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  if (!bounds_valid(chunk_bounds, total_tiles)) return hipErrorInvalidValue;
-  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, nullptr, nullptr, {}};
+  if (traced && d_tile_map != nullptr && d_tile_offsets == nullptr) return hipErrorInvalidDevicePointer;
+  if (!bounds_valid(chunk_bounds, total_work)) return hipErrorInvalidValue;
+  GroupedArgs args{d_problems, d_tile_offsets, d_work_offsets, problem_count, total_work, d_state,
+                   traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}};
   fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
-  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].grouped), dim3(grid),
-                         dim3(kThreads), params, 0, stream);
+  const KernelSet& k = kKernels[variant][path];
+  return hipLaunchKernel(reinterpret_cast<const void*>(traced ? k.traced[addressing] : k.grouped[addressing]),
+                         dim3(grid), dim3(k.threads), params, 0, stream);
 }
 
-hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
-                                     const int* d_tile_offsets, int problem_count, int total_tiles,
-                                     int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
-                                     long long* d_wg_clock, hipStream_t stream) {
-  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_tiles < 0) {
-    return hipErrorInvalidValue;
-  }
-  if (total_tiles == 0 || problem_count == 0) return hipSuccess;
-  if (d_problems == nullptr || d_tile_offsets == nullptr || d_state == nullptr) {
-    return hipErrorInvalidDevicePointer;
-  }
-  if (!bounds_valid(chunk_bounds, total_tiles)) return hipErrorInvalidValue;
-  GroupedArgs args{d_problems, d_tile_offsets, problem_count, total_tiles, d_state, d_tile_map, d_wg_clock, {}};
-  fill_bounds(args, chunk_bounds);
-  void* params[] = {&args};
-  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].traced), dim3(grid),
-                         dim3(kThreads), params, 0, stream);
+// 32-bit offsets from a work tile's origin reach every A and B value the
+// tile reads when 0 <= lda, 0 <= ldb, BM * lda < 2^30 and BK * ldb < 2^30;
+// the epilogue's per-lane offsets (a few rows of C or D) when 0 <= ldc, ldd
+// < 2^27 (ldc only matters when C is read).
+static bool fits_addr32(const KernelSet& k, const gg_device_problem_desc& p) {
+  constexpr int64_t kLimit = int64_t(1) << 30;
+  constexpr int64_t kLdLimit = int64_t(1) << 27;
+  const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+  return p.lda >= 0 && p.ldb >= 0 && (int64_t)k.bm * p.lda < kLimit && (int64_t)k.bk * p.ldb < kLimit &&
+         p.ldd >= 0 && p.ldd < kLdLimit && (!reads_c || (p.ldc >= 0 && p.ldc < kLdLimit));
+}
+
+hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out) {
+  if (!valid_kernel(variant, path) || out == nullptr) return hipErrorInvalidValue;
+  const KernelSet& k = kKernels[variant][path];
+  out->tiles_m = k.tm;
+  out->tiles_n = k.tn;
+  out->threads = k.threads;
+  out->rows = k.bm;
+  out->stage_k = k.bk;
+  return hipSuccess;
+}
+
+int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* problem) {
+  if (!valid_kernel(variant, path) || problem == nullptr) return -1;
+  if (problem->tiles_m <= 0 || problem->tiles_n <= 0) return 0;
+  return fits_addr32(kKernels[variant][path], *problem) ? 0 : 1;
+}
+
+hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
+                              const int* d_work_offsets, int problem_count, int total_work, int* d_state,
+                              const int* chunk_bounds, int grid, hipStream_t stream) {
+  return launch_grouped(variant, path, addressing, false, d_problems, nullptr, d_work_offsets, problem_count, total_work,
+                        d_state, chunk_bounds, grid, nullptr, nullptr, stream);
+}
+
+hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
+                                     const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
+                                     const int* d_work_offsets, int problem_count, int total_work, int* d_state,
+                                     const int* chunk_bounds, int grid, int* d_tile_map, long long* d_wg_clock,
+                                     hipStream_t stream) {
+  return launch_grouped(variant, path, addressing, true, d_problems, d_tile_offsets, d_work_offsets, problem_count,
+                        total_work, d_state, chunk_bounds, grid, d_tile_map, d_wg_clock, stream);
 }
 
 hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,
                              hipStream_t stream) {
   if (!valid_kernel(variant, path) || problem == nullptr) return hipErrorInvalidValue;
-  const int64_t tiles = (int64_t)problem->tiles_m * problem->tiles_n;
-  if (tiles <= 0) return hipSuccess;
-  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  const KernelSet& k = kKernels[variant][path];
+  if (problem->tiles_m <= 0 || problem->tiles_n <= 0) return hipSuccess;
+  const int64_t work = (int64_t)((problem->tiles_m + k.tm - 1) / k.tm) * ((problem->tiles_n + k.tn - 1) / k.tn);
+  if (work > 0x7fffffff) return hipErrorInvalidValue;
   gg_device_problem_desc p = *problem;
   void* params[] = {&p};
-  return hipLaunchKernel(reinterpret_cast<const void*>(kKernels[variant][path].single), dim3((unsigned)tiles),
-                         dim3(kThreads), params, 0, stream);
+  const int addressing = fits_addr32(k, p) ? GGK_ADDR_32 : GGK_ADDR_64;
+  return hipLaunchKernel(reinterpret_cast<const void*>(k.single[addressing]), dim3((unsigned)work),
+                         dim3(k.threads), params, 0, stream);
 }
 
 hipError_t ggk_kernel_resources_get(int kernel_kind, int variant, int path, ggk_kernel_resources* out) {
@@ -405,8 +479,8 @@ hipError_t ggk_kernel_resources_get(int kernel_kind, int variant, int path, ggk_
   gg_compiler_resources(kernel_kind, variant, path, &out->vgprs, &out->agprs, &out->sgprs,
                         &out->scratch_bytes_per_lane, &out->compiler_waves_per_simd, &out->lds_bytes);
   const void* fn = kernel_kind == GGK_KERNEL_GROUPED
-                       ? reinterpret_cast<const void*>(kKernels[variant][path].grouped)
-                       : reinterpret_cast<const void*>(kKernels[variant][path].single);
+                       ? reinterpret_cast<const void*>(kKernels[variant][path].grouped[GGK_ADDR_32])
+                       : reinterpret_cast<const void*>(kKernels[variant][path].single[GGK_ADDR_32]);
   hipFuncAttributes attr;
   hipError_t st = hipFuncGetAttributes(&attr, fn);
   if (st != hipSuccess) return st;
@@ -421,7 +495,8 @@ hipError_t ggk_kernel_resources_get(int kernel_kind, int variant, int path, ggk_
 hipError_t ggk_occupancy(int variant, int path, int* active_wgs_per_cu) {
   if (!valid_kernel(variant, path) || active_wgs_per_cu == nullptr) return hipErrorInvalidValue;
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      active_wgs_per_cu, reinterpret_cast<const void*>(kKernels[variant][path].grouped), kThreads, 0);
+      active_wgs_per_cu, reinterpret_cast<const void*>(kKernels[variant][path].grouped[GGK_ADDR_32]),
+      kKernels[variant][path].threads, 0);
 }
 
 hipError_t ggk_fill_uniform_f16(void* d_dst, int64_t count, uint64_t seed, uint64_t stream_id, float lo,

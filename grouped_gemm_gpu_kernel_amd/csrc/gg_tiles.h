@@ -20,13 +20,13 @@ namespace gg {
 // issued and stage k + 1 (issued DEPTH - 1 stages earlier) is written to the
 // other LDS buffer; one barrier closes the step.  The loop body is unrolled
 // DEPTH times so that every register set is addressed statically.
-template <class G, class Compute>
+template <class G, bool WIDE, class Compute>
 __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
                                            Compute&& compute) {
   constexpr int D = G::DEPTH;
   const int nk = (p.k + G::BK - 1) / G::BK;
   if (nk <= 0) return;
-  const StageLoader<G> loader(p, m0, n0);
+  const StageLoader<G, WIDE> loader(p, m0, n0);
   RawStage<G> ring[D];
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) {
@@ -49,8 +49,8 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
 }
 
 // ---------------------------------------------------------------------------
-// MFMA tile: v_mfma_f32_32x32x16_f16, 4 waves in a 2 x 2 grid, each wave owns a
-// (BM/2) x (BN/2) block of D held as (BM/64) x (BN/64) 32x32 accumulators.
+// MFMA tile: v_mfma_f32_32x32x16_f16, (BM/64) x (BN/64) waves, each owning a
+// 64 x 64 block of D held as 2 x 2 32x32 accumulators.
 //
 // Operand layouts of v_mfma_f32_32x32x16_f16 (lane l of 64):
 //   A: row l%32, k = 8*(l/32) + e, e = 0..7 (one 16-byte read of an A row)
@@ -65,20 +65,22 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
 // ---------------------------------------------------------------------------
 template <class G>
 struct MfmaTile {
-  static constexpr int WM = G::BM / 2;
-  static constexpr int WN = G::BN / 2;
+  static constexpr int WM = 64;
+  static constexpr int WN = 64;
+  static constexpr int WAVES_M = G::BM / WM;
+  static constexpr int WAVES_N = G::BN / WN;
   static constexpr int FM = WM / 32;
   static constexpr int FN = WN / 32;
-  static_assert(FM >= 1 && FN >= 1, "wave tile must hold whole 32x32 blocks");
+  static_assert(WAVES_M * WAVES_N * kWave == G::THREADS, "one wave per block of D");
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must hold whole 32x32 blocks");
 
-  // Multiplies one LDS stage into acc.  Every wave runs every MFMA of the
-  // stage, also over zero padding: a branch around the MFMAs would make the
-  // accumulators flow through control-flow joins, which costs a copy of all of
-  // them out of and back into the accumulation registers per stage.
+  // Multiplies one LDS stage into acc.  All MFMAs of a stage are issued
+  // unconditionally; skipping is decided once per tile for the whole wave.
   __device__ __forceinline__ static void compute_stage(const uint16_t* stage, int lane, int wm, int wn,
                                                        floatx16_t (&acc)[FM][FN]) {
     const uint16_t* as = stage;
     const uint16_t* bs = stage + G::A_STAGE;
+    lane = opaque_tid() & (kWave - 1);
     const int g = lane >> 4;
     const int j = lane & 15;
 #pragma unroll
@@ -110,15 +112,17 @@ struct MfmaTile {
     }
   }
 
-  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int tile_m, int tile_n,
-                                             uint16_t* lds) {
-    const int tid = threadIdx.x;
+  // Computes the work tile at (m0, n0).
+  template <bool WIDE>
+  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds) {
+    const int tid = opaque_tid();
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
-    const int m0 = tile_m * G::BM;
-    const int n0 = tile_n * G::BN;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm = wave / WAVES_N;
+    const int wn = wave % WAVES_N;
+    // A wave whose block starts past the problem's edge has nothing to
+    // multiply or store; it still stages its share of A and B for the others.
+    const bool live = m0 + wm * WM < p.m && n0 + wn * WN < p.n;
 
     floatx16_t acc[FM][FN];
 #pragma unroll
@@ -128,32 +132,87 @@ struct MfmaTile {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[fm][fn][e] = 0.0f;
 
-    run_k_loop<G>(p, m0, n0, lds, [&](const uint16_t* stage) { compute_stage(stage, lane, wm, wn, acc); });
+    run_k_loop<G, WIDE>(p, m0, n0, lds, [&](const uint16_t* stage) {
+      if (live) compute_stage(stage, lane, wm, wn, acc);
+    });
 
-    // A wave whose block starts past the problem's edge multiplied zeros and
-    // stores nothing.
-    if (m0 + wm * WM >= p.m || n0 + wn * WN >= p.n) return;
+    if (!live) return;
+    store_tile<WIDE>(p, m0 + wm * WM, n0 + wn * WN, lane, acc);
+  }
+
+  // 4 x 4 transpose across the 4 lanes of a quad: lane q holds x[k] = M[q][k]
+  // and receives M[k][q], in two exchange steps (partner q^1, then q^2).
+  __device__ __forceinline__ static void quad_transpose(float (&x)[4], int q) {
+    const bool odd = (q & 1) != 0;
+    const float s0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(odd ? x[0] : x[1]), 0xB1, 0xf, 0xf, true));
+    const float s1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(odd ? x[2] : x[3]), 0xB1, 0xf, 0xf, true));
+    float y[4];
+    y[0] = odd ? s0 : x[0];
+    y[1] = odd ? x[1] : s0;
+    y[2] = odd ? s1 : x[2];
+    y[3] = odd ? x[3] : s1;
+    const bool hi = (q & 2) != 0;
+    const float t0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi ? y[0] : y[2]), 0x4E, 0xf, 0xf, true));
+    const float t1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi ? y[1] : y[3]), 0x4E, 0xf, 0xf, true));
+    x[0] = hi ? t0 : y[0];
+    x[1] = hi ? t1 : y[1];
+    x[2] = hi ? y[2] : t0;
+    x[3] = hi ? y[3] : t1;
+  }
+
+  // D = alpha * acc + beta * C for the wave's block at (r0, c0).
+  //
+  // Accumulator element 4g + r of 32x32 block (fm, fn) is D[8g + 4h + r][c] of
+  // the block for lane (h, c) = (lane / 32, lane % 32).  A 4 x 4 transpose in
+  // each quad of lanes (c = 4j .. 4j+3) gives lane (h, 4j + q) row 8g + 4h + q,
+  // columns 4j .. 4j+3, so C is read and D written as 16-byte vectors: a
+  // dword access costs the address unit as much as a 16-byte one.  Columns
+  // that cross N go element by element.  With 32-bit addressing each access
+  // is a wave-uniform 64-bit row origin plus a per-lane 32-bit offset.
+  template <bool WIDE>
+  __device__ __forceinline__ static void store_tile(const gg_device_problem_desc& p, int r0, int c0, int lane,
+                                                    const floatx16_t (&acc)[FM][FN]) {
     const bool use_c = p.c != nullptr && p.beta != 0.0f;
-    g_cf32_t* cptr = (g_cf32_t*)p.c;
-    g_f32_t* dptr = (g_f32_t*)p.d;
+    const int q = lane & 3;
+    const int lrow = 4 * (lane >> 5) + q;  // row within an 8-row group
+    const int lcol = (lane & 31) & ~3;     // first column of the lane's vector
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
-        const int col = n0 + wn * WN + fn * 32 + (lane & 31);
-        const int row0 = m0 + wm * WM + fm * 32 + 4 * (lane >> 5);
-        const bool col_ok = col < p.n;
-        float cv[16];
+        const int col = c0 + fn * 32 + lcol;
+        const int ncol = p.n - col;  // columns of the vector inside the matrix
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = row0 + 8 * (e >> 2) + (e & 3);
-          cv[e] = (use_c && col_ok && row < p.m) ? cptr[(int64_t)row * p.ldc + col] : 0.0f;
-        }
+        for (int g = 0; g < 4; ++g) {
+          float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                        acc[fm][fn][4 * g + 3]};
+          quad_transpose(v, q);
+          const int urow = r0 + fm * 32 + 8 * g;  // wave-uniform
+          const int row = urow + lrow;
+          if (row >= p.m || ncol <= 0) continue;
+          g_cf32_t* crow;
+          g_f32_t* drow;
+          if constexpr (WIDE) {
+            crow = (g_cf32_t*)p.c + ((int64_t)row * p.ldc + col);
+            drow = (g_f32_t*)p.d + ((int64_t)row * p.ldd + col);
+          } else {
+            crow = (g_cf32_t*)p.c + ((int64_t)urow * p.ldc + c0) + (uint32_t)(lrow * p.ldc + fn * 32 + lcol);
+            drow = (g_f32_t*)p.d + ((int64_t)urow * p.ldd + c0) + (uint32_t)(lrow * p.ldd + fn * 32 + lcol);
+          }
+          if (ncol >= 4) {
+            floatx4_t cv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (use_c) cv = *(const __attribute__((address_space(1))) floatx4_t*)crow;
+            floatx4_t out;
+            out[0] = epilogue_value(v[0], cv[0], p.alpha, p.beta);
+            out[1] = epilogue_value(v[1], cv[1], p.alpha, p.beta);
+            out[2] = epilogue_value(v[2], cv[2], p.alpha, p.beta);
+            out[3] = epilogue_value(v[3], cv[3], p.alpha, p.beta);
+            *(__attribute__((address_space(1))) floatx4_t*)drow = out;
+          } else {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = row0 + 8 * (e >> 2) + (e & 3);
-          if (col_ok && row < p.m) {
-            dptr[(int64_t)row * p.ldd + col] = epilogue_value(acc[fm][fn][e], cv[e], p.alpha, p.beta);
+            for (int e = 0; e < 3; ++e) {
+              if (e < ncol) drow[e] = epilogue_value(v[e], use_c ? crow[e] : 0.0f, p.alpha, p.beta);
+            }
           }
         }
       }
@@ -174,6 +233,7 @@ struct FmaTile {
   static constexpr int RM = G::BM / 16;
   static constexpr int RN = G::BN / 16;
   static_assert(RN == 4 || RN == 8, "column block must be one or two LDS chunks");
+  static_assert(G::THREADS == 256, "16 x 16 thread grid");
 
   __device__ __forceinline__ static void compute_stage(const uint16_t* stage, int krem, int tm, int tn,
                                                        float (&acc)[RM][RN]) {
@@ -210,13 +270,12 @@ struct FmaTile {
     }
   }
 
-  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int tile_m, int tile_n,
-                                             uint16_t* lds) {
+  // Computes the work tile at (m0, n0).
+  template <bool WIDE>
+  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds) {
     const int tid = threadIdx.x;
     const int tm = tid >> 4;
     const int tn = tid & 15;
-    const int m0 = tile_m * G::BM;
-    const int n0 = tile_n * G::BN;
     // Wave w holds tm = 4w .. 4w+3, i.e. rows [4w*RM, 4w*RM + 4*RM) of the tile.
     const bool active = m0 + (tid / kWave) * 4 * RM < p.m;
 
@@ -227,7 +286,7 @@ struct FmaTile {
       for (int j = 0; j < RN; ++j) acc[i][j] = 0.0f;
 
     int kt = 0;
-    run_k_loop<G>(p, m0, n0, lds, [&](const uint16_t* stage) {
+    run_k_loop<G, WIDE>(p, m0, n0, lds, [&](const uint16_t* stage) {
       if (active) compute_stage(stage, p.k - kt * G::BK, tm, tn, acc);
       ++kt;
     });

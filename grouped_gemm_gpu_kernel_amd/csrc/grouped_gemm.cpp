@@ -23,6 +23,7 @@ constexpr int kWaveSize = 64;
 constexpr int kRegsPerLanePerSimd = 512;
 constexpr int kRegAllocGranule = 8;
 constexpr int kMaxWavesPerSimd = 8;
+constexpr int kSimdsPerCu = 4;
 
 int ceil_div(int x, int y) { return (x + y - 1) / y; }
 
@@ -39,6 +40,7 @@ struct RuntimeMode {
   int variant = -1;
   int path = GGK_PATH_FMA;
   ggk_device_info device{};
+  ggk_work_shape work{};
 };
 
 // resolve_runtime_mode (src/grouped_gemm.cu:111-143): unsupported shapes are
@@ -47,29 +49,30 @@ struct RuntimeMode {
 hipError_t resolve_runtime_mode(const KernelConfig& config, RuntimeMode* mode) {
   const int variant = resolve_variant(config);
   if (variant < 0) return hipErrorInvalidValue;
-  const hipError_t status = ggk_device_info_get(&mode->device);
+  hipError_t status = ggk_device_info_get(&mode->device);
   if (status != hipSuccess) return status;
   mode->variant = variant;
   mode->path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;
-  return hipSuccess;
+  return ggk_work_shape_get(mode->variant, mode->path, &mode->work);
 }
 
 // Formula estimate of registers per lane (the role of
 // estimated_*_registers_per_thread, src/grouped_gemm.cu:175-217), for this
-// build's tiles.  MFMA: the (BM*BN/256) float accumulators a lane holds, its
-// A/B operand fragments (4 registers per 32-row or 32-column block), the
-// staged global pieces (7 registers each) and ~24 for addresses and loop state.
-// FMA: RM*RN accumulators, RM 16-byte A slices, RN B values, staging, ~24.
-int estimated_registers_per_thread(const KernelConfig& config, bool mfma) {
-  const int bm = config.cta_m;
-  const int bn = config.cta_n;
-  const int bk = 32;  // internal stage depth of every variant
-  const int pieces = (bm * bk / 8 + bk * bn / 8) / kThreadsPerBlock;
+// build's kernels.  Work tile BM x BN (a block of tiles_m x tiles_n
+// macro-tiles), stage depth 64, T threads; a staged global piece holds 5
+// registers plus 2 of offsets.  MFMA: BM*BN/T float accumulators, two A and
+// two B operand fragments of 4 registers, staging, ~24 for addresses and loop
+// state.  FMA: RM*RN accumulators, RM 16-byte A slices, RN B values, staging, ~24.
+int estimated_registers_per_thread(const KernelConfig& config, const ggk_work_shape& work, bool mfma) {
+  const int bm = config.cta_m * work.tiles_m;
+  const int bn = config.cta_n * work.tiles_n;
+  const int bk = 64;
+  const int threads = work.threads > 0 ? work.threads : kThreadsPerBlock;
+  const int pieces = (bm * bk / 8 + bk * bn / 8) / threads;
   const int staging = pieces * 7;
   if (mfma) {
-    const int acc = bm * bn / kThreadsPerBlock;
-    const int fragments = 4 * (bm / 64) + 4 * (bn / 64);
-    return acc + fragments + staging + 24;
+    const int acc = bm * bn / threads;
+    return acc + 16 + staging + 24;
   }
   const int rm = bm / 16;
   const int rn = bn / 16;
@@ -81,17 +84,19 @@ int round_up(int x, int granule) { return (x + granule - 1) / granule * granule;
 hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, OccupancyInfo* info) {
   const ggk_device_info& dev = mode.device;
   const bool mfma = mode.path == GGK_PATH_MFMA;
+  const int wave = dev.wave_size > 0 ? dev.wave_size : kWaveSize;
+  const int threads = mode.work.threads > 0 ? mode.work.threads : kThreadsPerBlock;
   *info = OccupancyInfo{};
   info->sm_count = dev.compute_units;
   info->max_blocks_per_sm = dev.max_wgs_per_cu;
-  info->threads_per_block = kThreadsPerBlock;
+  info->threads_per_block = threads;
   info->max_threads_per_sm = dev.max_threads_per_cu;
-  info->warps_per_block = kThreadsPerBlock / (dev.wave_size > 0 ? dev.wave_size : kWaveSize);
-  info->max_warps_per_sm = dev.max_threads_per_cu / (dev.wave_size > 0 ? dev.wave_size : kWaveSize);
+  info->warps_per_block = threads / wave;
+  info->max_warps_per_sm = dev.max_threads_per_cu / wave;
   info->max_registers_per_sm = dev.regs_per_cu;
   info->max_registers_per_block = dev.regs_per_block;
-  info->estimated_registers_per_thread = estimated_registers_per_thread(config, mfma);
-  info->estimated_registers_per_block = info->estimated_registers_per_thread * kThreadsPerBlock;
+  info->estimated_registers_per_thread = estimated_registers_per_thread(config, mode.work, mfma);
+  info->estimated_registers_per_block = info->estimated_registers_per_thread * threads;
   info->using_tensor_cores = mfma;
 
   ggk_kernel_resources res{};
@@ -108,16 +113,18 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
   // unavailable, fall back to what hipFuncGetAttributes reports.
   const int regs = (res.vgprs + res.agprs) > 0 ? res.vgprs + res.agprs : res.num_regs;
   info->registers_per_thread = regs;
-  info->registers_per_block = regs * kThreadsPerBlock;
+  info->registers_per_block = regs * threads;
   info->static_shared_bytes = res.lds_static > 0 ? res.lds_static : res.lds_bytes;
   info->dynamic_shared_bytes = res.lds_dynamic;
 
-  // A workgroup's 4 waves sit one per SIMD, so resident workgroups per CU are
-  // limited by waves per SIMD (registers), by LDS and by the wave slots.
+  // A workgroup's waves are spread evenly over the 4 SIMDs of a CU, so
+  // resident workgroups per CU are limited by waves per SIMD (registers), by
+  // LDS and by the wave slots.
   const int waves_per_simd =
       regs > 0 ? std::min(kMaxWavesPerSimd, kRegsPerLanePerSimd / round_up(regs, kRegAllocGranule))
                : kMaxWavesPerSimd;
-  info->register_limited_blocks_per_sm = waves_per_simd;
+  const int block_waves_per_simd = std::max(1, ceil_div(info->warps_per_block, kSimdsPerCu));
+  info->register_limited_blocks_per_sm = waves_per_simd / block_waves_per_simd;
   const int lds_per_block = info->static_shared_bytes + info->dynamic_shared_bytes;
   info->lds_limited_blocks_per_sm =
       lds_per_block > 0 ? dev.lds_per_cu / lds_per_block : info->max_blocks_per_sm;
@@ -132,13 +139,12 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
   return hipSuccess;
 }
 
-// Splits the tile indices [0, total) into GGK_SCHEDULER_CHUNKS contiguous
-// chunks of about equal memory cost, one per XCD.  A tile of problem p moves
-// (BM + BN) * k binary16 values in and BM * BN floats out (twice when C is
-// read); the grouped kernel on these shapes is bound by those bytes.
+// Splits the work-tile indices [0, total) into GGK_SCHEDULER_CHUNKS contiguous
+// chunks of about equal memory cost, one per XCD.  A work tile of problem p
+// moves up to (BM + BN) * k binary16 values in and BM * BN floats out (twice
+// when C is read); the grouped kernel on these shapes is bound by those bytes.
 std::array<int, GGK_SCHEDULER_CHUNKS + 1> plan_chunks(const std::vector<DeviceProblemDesc>& problems,
-                                                      const std::vector<int>& offsets,
-                                                      const KernelConfig& config) {
+                                                      const std::vector<int>& offsets, int bm, int bn) {
   constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
   std::array<int, kChunks + 1> bounds{};
   const int total = offsets.back();
@@ -147,13 +153,14 @@ std::array<int, GGK_SCHEDULER_CHUNKS + 1> plan_chunks(const std::vector<DevicePr
   for (size_t i = 0; i < problems.size(); ++i) {
     const DeviceProblemDesc& p = problems[i];
     const bool reads_c = p.c != nullptr && p.beta != 0.0f;
-    cost[i] = 2.0 * (config.cta_m + config.cta_n) * std::max(p.k, 0) +
-              4.0 * config.cta_m * config.cta_n * (reads_c ? 2.0 : 1.0);
+    const double rows = std::min(bm, std::max(p.m, 0));
+    const double cols = std::min(bn, std::max(p.n, 0));
+    cost[i] = 2.0 * (rows + cols) * std::max(p.k, 0) + 4.0 * rows * cols * (reads_c ? 2.0 : 1.0);
     sum += cost[i] * (offsets[i + 1] - offsets[i]);
   }
   bounds[0] = 0;
   bounds[kChunks] = total;
-  double before = 0.0;  // cost of all tiles of problems before i
+  double before = 0.0;  // cost of all work tiles of problems before i
   size_t i = 0;
   for (int c = 1; c < kChunks; ++c) {
     const double target = sum * c / kChunks;
@@ -294,16 +301,19 @@ hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info) {
 
 struct GroupedGemmExecutor::Impl {
   DeviceProblemDesc* d_problems = nullptr;
-  int* d_tile_offsets = nullptr;
+  int* d_tile_offsets = nullptr;  // [problem_count + 1] reference tile offsets, then
+                                  // [problem_count + 1] work-tile offsets
   int* d_state = nullptr;
 
   int problem_count = 0;
   int total_tiles = 0;
+  int total_work = 0;
   int grid_ctas = 0;
 
   KernelConfig config{};
   int variant = -1;
   int path = GGK_PATH_FMA;
+  int addressing = GGK_ADDR_32;
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> chunk_bounds{};
 };
 
@@ -350,13 +360,19 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
   impl_->problem_count = problem_count;
   impl_->total_tiles = prepared.total_tiles;
+  impl_->total_work = 0;
   impl_->grid_ctas = 0;
+  impl_->addressing = GGK_ADDR_32;
   impl_->config = config;
   impl_->variant = mode.variant;
   impl_->path = mode.path;
 
   std::vector<DeviceProblemDesc> device_problems;
   device_problems.reserve(problem_count);
+  // Reference tile offsets followed by the work-tile offsets of the same order.
+  std::vector<int> offsets(prepared.tile_offsets);
+  offsets.reserve(2 * (problem_count + 1));
+  offsets.push_back(0);
   if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
   for (int i = 0; i < problem_count; ++i) {
     const ProblemDesc& p = prepared.sorted_problems[i];
@@ -367,8 +383,14 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
       return hipErrorInvalidValue;
     }
+    const int64_t work = static_cast<int64_t>(ceil_div(dp.tiles_m, mode.work.tiles_m)) *
+                         ceil_div(dp.tiles_n, mode.work.tiles_n);
+    offsets.push_back(static_cast<int>(offsets.back() + work));  // never above the tile count
+    if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
     device_problems.push_back(dp);
   }
+  const std::vector<int> work_offsets(offsets.begin() + problem_count + 1, offsets.end());
+  impl_->total_work = work_offsets.back();
 
   if (problem_count > 0) {
     status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems),
@@ -377,10 +399,9 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     status = ggk_copy_to_device(impl_->d_problems, device_problems.data(),
                                 problem_count * sizeof(DeviceProblemDesc));
     if (status != hipSuccess) return status;
-    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_tile_offsets), (problem_count + 1) * sizeof(int));
+    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_tile_offsets), offsets.size() * sizeof(int));
     if (status != hipSuccess) return status;
-    status = ggk_copy_to_device(impl_->d_tile_offsets, prepared.tile_offsets.data(),
-                                (problem_count + 1) * sizeof(int));
+    status = ggk_copy_to_device(impl_->d_tile_offsets, offsets.data(), offsets.size() * sizeof(int));
     if (status != hipSuccess) return status;
   }
   if (impl_->total_tiles > 0) {
@@ -390,12 +411,14 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (status != hipSuccess) return status;
   }
 
-  impl_->chunk_bounds = plan_chunks(device_problems, prepared.tile_offsets, config);
+  impl_->chunk_bounds = plan_chunks(device_problems, work_offsets, config.cta_m * mode.work.tiles_m,
+                                    config.cta_n * mode.work.tiles_n);
 
   OccupancyInfo occupancy{};
   status = fill_occupancy(config, mode, &occupancy);
   if (status != hipSuccess) return status;
-  impl_->grid_ctas = grid_ctas_for(impl_->total_tiles, config, occupancy);
+  // The persistent grid is sized by the units it claims: work tiles.
+  impl_->grid_ctas = grid_ctas_for(impl_->total_work, config, occupancy);
   return hipSuccess;
 }
 
@@ -405,18 +428,20 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
 hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
-  return ggk_launch_grouped(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
-                            impl_->problem_count, impl_->total_tiles, impl_->d_state,
-                            impl_->chunk_bounds.data(), impl_->grid_ctas, stream);
+  return ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
+                            impl_->d_tile_offsets + impl_->problem_count + 1, impl_->problem_count,
+                            impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(), impl_->grid_ctas,
+                            stream);
 }
 
 hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
-  return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->d_problems, impl_->d_tile_offsets,
-                                   impl_->problem_count, impl_->total_tiles, impl_->d_state,
-                                   impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map, d_wg_clock,
-                                   stream);
+  return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
+                                   impl_->d_tile_offsets,
+                                   impl_->d_tile_offsets + impl_->problem_count + 1, impl_->problem_count,
+                                   impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(),
+                                   impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
 }
 
 int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }

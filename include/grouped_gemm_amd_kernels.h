@@ -121,28 +121,60 @@ hipError_t ggk_device_synchronize(void);
  * 1024-1083). */
 hipError_t ggk_device_info_get(ggk_device_info* out);
 
+/* Work tile of a kernel: one claim of the grouped kernel, or one workgroup of
+ * the single-problem kernel, computes a tiles_m x tiles_n block of the
+ * variant's macro-tiles (src/grouped_gemm.cu:54-65) with `threads` threads;
+ * rows = tiles_m * cta_m, and stage_k is the depth of one LDS stage.
+ * The work-tile count of a problem is ceil(tiles_m_p / tiles_m) *
+ * ceil(tiles_n_p / tiles_n), numbered row-major; the reference tile (tm, tn)
+ * belongs to work tile (tm / tiles_m, tn / tiles_n).  No reference
+ * counterpart: the reference computes one macro-tile per CTA. */
+typedef struct ggk_work_shape {
+  int tiles_m;
+  int tiles_n;
+  int threads;
+  int rows;
+  int stage_k;
+} ggk_work_shape;
+hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out);
+
+/* Addressing form of a grouped launch.  GGK_ADDR_32: A and B are addressed
+ * and C/D with 32-bit offsets from per-tile origins, which needs, for every
+ * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda < 2^30, stage_k * ldb
+ * < 2^30 (ggk_work_shape), 0 <= ldd < 2^27 and, when C is read (c != NULL and
+ * beta != 0), 0 <= ldc < 2^27.  GGK_ADDR_64: 64-bit addresses, any layout, slower.
+ * ggk_needs_addr64 returns 1 when `problem` (host memory) needs GGK_ADDR_64,
+ * 0 when not (also for a problem without tiles), -1 for a bad argument.  The
+ * single-problem launch chooses by itself.  No reference counterpart. */
+enum { GGK_ADDR_32 = 0, GGK_ADDR_64 = 1 };
+int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* problem);
+
 /* Persistent grouped launch (launch_grouped_by_variant + grouped_gemm_kernel,
  * src/grouped_gemm.cu:640-675, 728-751, 800-869).  d_problems[problem_count]
- * in sorted order, d_tile_offsets[problem_count + 1], d_state holds
+ * in sorted order; d_work_offsets[problem_count + 1] is the prefix sum of the
+ * problems' work-tile counts (the role of the reference's d_tile_offsets,
+ * which it equals when the work tile is one macro-tile); d_state holds
  * GGK_SCHEDULER_STATE_INTS zeroed ints.  chunk_bounds (host memory,
- * GGK_SCHEDULER_CHUNKS + 1 non-decreasing ints from 0 to total_tiles, or NULL
- * for equal tile counts) splits the tile indices into the per-XCD chunks.
- * grid workgroups of 256 threads each claim tiles until total_tiles are done. */
-hipError_t ggk_launch_grouped(int variant, int path, const gg_device_problem_desc* d_problems,
-                              const int* d_tile_offsets, int problem_count, int total_tiles,
-                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream);
+ * GGK_SCHEDULER_CHUNKS + 1 non-decreasing ints from 0 to total_work, or NULL
+ * for equal counts) splits the work-tile indices into the per-XCD chunks.
+ * grid workgroups claim work tiles until total_work are done. */
+hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
+                              const int* d_work_offsets, int problem_count, int total_work, int* d_state,
+                              const int* chunk_bounds, int grid, hipStream_t stream);
 
-/* The same scheduler with instrumentation.  d_tile_map (may be NULL): for each
- * claimed tile t, ints [3t, 3t+3) receive (problem, tile_m, tile_n) and no
- * GEMM is computed.  d_wg_clock (may be NULL): for workgroup w, the
- * 100 MHz wall clock at its start and at the end of its last tile go to
- * [2w, 2w+2); the GEMM is computed as usual. */
-hipError_t ggk_launch_grouped_traced(int variant, int path, const gg_device_problem_desc* d_problems,
-                                     const int* d_tile_offsets, int problem_count, int total_tiles,
-                                     int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
-                                     long long* d_wg_clock, hipStream_t stream);
+/* The same scheduler with instrumentation.  d_tile_map (may be NULL; needs
+ * d_tile_offsets, the reference tile offsets): for each reference tile t of a
+ * claimed work tile, ints [3t, 3t+3) receive (problem, tile_m, tile_n) and no
+ * GEMM is computed.  d_wg_clock (may be NULL): for workgroup w, the 100 MHz
+ * wall clock at its start and at the end of its last tile go to [2w, 2w+2);
+ * the GEMM is computed as usual. */
+hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
+                                     const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
+                                     const int* d_work_offsets, int problem_count, int total_work, int* d_state,
+                                     const int* chunk_bounds, int grid, int* d_tile_map, long long* d_wg_clock,
+                                     hipStream_t stream);
 
-/* One problem, one workgroup per tile, row-major tile order
+/* One problem, one workgroup per work tile, row-major work-tile order
  * (single_problem_gemm_kernel + launch_single_problem_variant,
  * src/grouped_gemm.cu:677-688, 753-769).  *problem is read on the host and
  * passed by value; a problem with zero tiles launches nothing. */

@@ -54,3 +54,39 @@ def test_cpp_api_header_mirrors_reference_names():
                  "query_occupancy(", "run_grouped_gemm_once(", "run_baseline_per_problem(",
                  "count_non_empty_problems(", "DeviceProblemDesc"):
         assert name in text, name
+
+
+def test_addressing_form_classifier():
+    """ggk_needs_addr64 (host-only) picks 64-bit addressing exactly when a problem's tile offsets would
+    not fit 32 bits: work-tile rows * lda >= 2^30 or 64 * ldb >= 2^30, or a negative leading dimension."""
+    lib = _lib.lib()
+    shape = _lib.GGKWorkShape()
+
+    def needs(variant, path, lda, ldb, tiles=1, ldc=1, ldd=1, c=None, beta=0.0):
+        p = _lib.GGDeviceProblemDesc(m=1, n=1, k=1, c=c, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd, beta=beta,
+                                     tiles_m=tiles, tiles_n=tiles)
+        return lib.ggk_needs_addr64(variant, path, p)
+
+    for variant, cta_m in ((_lib.GGK_VARIANT_64x64x16, 64), (_lib.GGK_VARIANT_128x64x32, 128),
+                           (_lib.GGK_VARIANT_64x128x32, 64)):
+        for path in (_lib.GGK_PATH_FMA, _lib.GGK_PATH_MFMA):
+            assert lib.ggk_work_shape_get(variant, path, shape) == 0
+            assert shape.rows == cta_m * shape.tiles_m and shape.stage_k in (32, 64)
+            limit_a = (1 << 30) // shape.rows
+            limit_b = (1 << 30) // shape.stage_k
+            assert needs(variant, path, limit_a - 1, 8) == 0
+            assert needs(variant, path, limit_a, 8) == 1
+            assert needs(variant, path, 8, limit_b - 1) == 0
+            assert needs(variant, path, 8, limit_b) == 1
+            assert needs(variant, path, -1, 8) == 1 and needs(variant, path, 8, -1) == 1
+            assert needs(variant, path, 1 << 30, 1 << 30, tiles=0) == 0  # no tiles, nothing addressed
+            assert needs(variant, path, 8, 8, ldd=(1 << 27) - 1) == 0
+            assert needs(variant, path, 8, 8, ldd=1 << 27) == 1
+            # ldc matters only when C is read
+            assert needs(variant, path, 8, 8, ldc=1 << 27) == 0
+            assert needs(variant, path, 8, 8, ldc=1 << 27, c=64, beta=0.0) == 0
+            assert needs(variant, path, 8, 8, ldc=1 << 27, c=64, beta=0.5) == 1
+            assert needs(variant, path, 8, 8, ldc=(1 << 27) - 1, c=64, beta=0.5) == 0
+    assert lib.ggk_needs_addr64(7, 0, _lib.GGDeviceProblemDesc()) == -1
+    assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_128x64x32, _lib.GGK_PATH_MFMA, shape) == 0
+    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 2, 512, 256, 64)

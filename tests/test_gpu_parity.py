@@ -201,14 +201,19 @@ def test_grid_size_and_occupancy(torch):
             assert st == 0
             say(f"occupancy {config} mfma={mfma}: {info}")
             assert info.sm_count == 256 and info.using_tensor_cores == mfma
-            assert info.warps_per_block == 4 and info.max_warps_per_sm == 32
+            # MFMA kernels compute 2 x 2 reference tiles per workgroup with one wave per 64 x 64
+            # block of D; the FMA kernels use 256 threads.
+            want_threads = (2 * cfg.cta_m // 64) * (2 * cfg.cta_n // 64) * 64 if mfma else 256
+            assert info.threads_per_block == want_threads
+            assert info.warps_per_block == want_threads // 64 and info.max_warps_per_sm == 32
             assert info.registers_per_thread > 0 and info.active_blocks_per_sm >= 1
             # The runtime's occupancy calculator and the register/LDS accounting must agree on the
             # binding limit.
             assert info.active_blocks_per_sm == min(info.register_limited_blocks_per_sm,
                                                     info.lds_limited_blocks_per_sm,
                                                     info.wave_limited_blocks_per_sm)
-            assert info.theoretical_occupancy == pytest.approx(info.active_blocks_per_sm * 4 / 32)
+            assert info.theoretical_occupancy == pytest.approx(
+                info.active_blocks_per_sm * info.warps_per_block / 32)
             for total in (1, 100, 255, 256, 257, 5000, 100000):
                 for persistent in (0, 1, 999):
                     c2 = KernelConfig.named(config, use_tensor_cores=mfma, persistent_ctas=persistent)
@@ -311,6 +316,44 @@ def test_padded_leading_dimensions(torch):
                 tol = tolerance(k, 1.0, 1.0, 1.0, 0.5, -1.25)
                 assert np.abs(got[:, :n] - want[:, :n]).max() <= tol
                 assert np.isnan(got[:, n:]).all(), "padding columns of D were written"
+
+
+def test_wide_leading_dimensions(torch):
+    """Leading dimensions too large for 32-bit tile offsets (lda * 256 >= 2^30, ldb * 64 >= 2^30) select
+    the 64-bit addressing kernels, in a grouped launch mixed with ordinary problems and per problem."""
+    wide_lda, wide_ldb = (1 << 24) + 3, (1 << 25) + 1  # wide for every work-tile shape
+    shapes = [(3, 70, 21, wide_lda, 70), (40, 9, 5, 21, wide_ldb), (65, 130, 77, 77, 130)]
+    store, probs, dense = [], [], []
+    for i, (m, n, k, lda, ldb) in enumerate(shapes):
+        a = torch.empty((m - 1) * lda + k + 1, dtype=torch.float16, device="cuda")
+        b = torch.empty((k - 1) * ldb + n + 1, dtype=torch.float16, device="cuda")
+        a.uniform_(-1, 1)
+        b.uniform_(-1, 1)
+        c = torch.empty(m * n, dtype=torch.float32, device="cuda").uniform_(-1, 1)
+        d = torch.full((m * n,), float("nan"), device="cuda")
+        # Matrices start 2 bytes into their buffers: odd element offsets exercise the realignment.
+        ah = torch.as_strided(a, (m, k), (lda, 1), 1).cpu().numpy().view(np.uint16)
+        bh = torch.as_strided(b, (k, n), (ldb, 1), 1).cpu().numpy().view(np.uint16)
+        store += [a, b, c, d]
+        dense.append((ah.reshape(-1).copy(), bh.reshape(-1).copy(), c.cpu().numpy()))
+        probs.append(ProblemDesc(m, n, k, a.data_ptr() + 2, b.data_ptr() + 2, c.data_ptr(), d.data_ptr(),
+                                 lda, ldb, n, n, 1.5, 0.25))
+    for mfma in PATHS:
+        for config in CONFIGS:
+            cfg = KernelConfig.named(config, use_tensor_cores=mfma)
+            for run in ("grouped", "baseline"):
+                for dd in store[3::4]:
+                    dd.fill_(float("nan"))
+                if run == "grouped":
+                    assert api.run_grouped_gemm_once(probs, SortMode.kByTiles, cfg) == 0
+                else:
+                    assert api.run_baseline_per_problem(probs, cfg) == 0
+                torch.cuda.synchronize()
+                for (m, n, k, _, _), (ah, bh, ch), dd in zip(shapes, dense, store[3::4]):
+                    got = dd.cpu().numpy()
+                    want = O.gemm(m, n, k, ah, k, bh, n, ch, n, 1.5, 0.25)
+                    assert np.abs(got - want).max() <= tolerance(k, 1.0, 1.0, 1.0, 1.5, 0.25), \
+                        f"{config} mfma={mfma} {run} {(m, n, k)}"
 
 
 def test_persistent_grid_sizes_and_repeated_runs(torch):

@@ -42,6 +42,9 @@ def parse_args():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB a few times (for scaling HBM "
                          "byte counters of a profiler run) and exit")
+    ap.add_argument("--profile-summary", nargs="+", metavar="DIR",
+                    help="only summarize rocprofv3 CSV output folders (kernel trace and/or counters) and exit")
+    ap.add_argument("--kernel", default="gg_grouped_kernel", help="kernel-name filter for --profile-summary")
     return ap.parse_args()
 
 
@@ -57,7 +60,8 @@ def calibrate_copy(torch, mib: int) -> int:
 
 
 def time_runs(torch, fn, steps: int, warmup: int) -> float:
-    """Mean ms per call over `steps` calls after `warmup`, HIP events on the current stream."""
+    """Mean ms per call over `steps` calls after `warmup`, HIP events on the current stream (the
+    stream fn launches on)."""
     for _ in range(warmup):
         st = fn()
         if st != 0:
@@ -125,8 +129,73 @@ def cpu_baseline(dw, spec, seconds: float):
     }
 
 
+def _csv_rows(path: Path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def profile_summary(dirs, kernel_filter: str) -> int:
+    """Prints what a rocprofv3 --output-format csv folder holds for kernels matching kernel_filter:
+    dispatch count and mean/min/max duration (kernel trace), mean counter value per dispatch
+    (counter collection)."""
+    import re
+    pat = re.compile(kernel_filter)
+    for d in dirs:
+        d = Path(d)
+        print(f"== {d}")
+        for trace in sorted(d.rglob("*kernel_trace.csv")):
+            groups = {}
+            for r in _csv_rows(trace):
+                name = r.get("Kernel_Name", "")
+                if not pat.search(name):
+                    continue
+                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # us
+                groups.setdefault(name, []).append(dur)
+            for name, durs in groups.items():
+                print(f"kernel {name}")
+                print(f"  dispatches {len(durs)}  mean_us {sum(durs) / len(durs):.2f}  "
+                      f"min_us {min(durs):.2f}  max_us {max(durs):.2f}")
+                print(f"  durations_us {' '.join(f'{x:.1f}' for x in durs)}")
+        for cc in sorted(d.rglob("*counter_collection.csv")):
+            per = {}
+            for r in _csv_rows(cc):
+                name = r.get("Kernel_Name", "")
+                if not pat.search(name):
+                    continue
+                per.setdefault((name, r["Counter_Name"]), {}).setdefault(r["Dispatch_Id"], 0.0)
+                per[(name, r["Counter_Name"])][r["Dispatch_Id"]] += float(r["Counter_Value"])
+            for (name, counter), vals in per.items():
+                v = list(vals.values())
+                print(f"counter {counter} kernel {name}")
+                print(f"  dispatches {len(v)}  mean_per_dispatch {sum(v) / len(v):.6g}  "
+                      f"min {min(v):.6g}  max {max(v):.6g}")
+    return 0
+
+
+def committed_traffic(workload: str):
+    """HBM bytes per launch of the grouped kernel on `workload`, from the committed rocprofv3 summary
+    profiles/gg_grouped_kernel_<workload>_hbm_traffic.txt (FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by the same counter's reading for a plain copy of known size), or None."""
+    path = ROOT / "profiles" / f"gg_grouped_kernel_{workload}_hbm_traffic.txt"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return {"bytes": float(vals["traffic_bytes_per_launch"]), "mode": vals.get("sort_mode", ""),
+                "source": str(path.relative_to(ROOT))}
+    except (KeyError, ValueError):
+        return None
+
+
 def main() -> int:
     args = parse_args()
+    if args.profile_summary:
+        return profile_summary(args.profile_summary, args.kernel)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the grouped GEMM shards "
               "problems across GPUs with no exchange step, see the design notes.", file=sys.stderr)
@@ -155,7 +224,10 @@ def main() -> int:
     modes = [SortMode(int(x)) for x in args.modes.split(",")]
     per_mode = []
     best = None
-    stream = torch.cuda.current_stream()
+    # A stream of our own at default priority: the events that time a run are recorded on the stream
+    # the kernel is launched on.
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     for mode in modes:
         t0 = time.perf_counter()
         prep = api.prepare_problem_set(probs, cfg, mode)
@@ -196,12 +268,16 @@ def main() -> int:
     hbm_frac = achieved_gbs / HBM_PEAK_GBS
     ridge = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     bound = "hbm" if flops / algo_bytes < ridge else "mfma"
+    traffic = committed_traffic(spec.name) if not args.fma else None
     if bound == "hbm":
         roofline = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(hbm_frac, 4), "traffic": None}
+                    "frac": round(hbm_frac, 4), "traffic": round(traffic["bytes"]) if traffic else None}
     else:
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(mfma_frac, 4), "traffic": None}
+                    "frac": round(mfma_frac, 4), "traffic": round(traffic["bytes"]) if traffic else None}
+    if traffic:
+        roofline["traffic_source"] = f"{traffic['source']} ({traffic['mode']})"
+        roofline["algorithmic_bytes"] = algo_bytes
     out = {
         "metric": "grouped TFLOP/s + % FP16 MFMA peak on mixed-512, 1 MI355X; tail_share",
         "value": round(tflops, 2),
@@ -213,10 +289,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 in, fp32 accumulate",
+        "dtype": "fp16",
         "data": "synthetic (seeded; shapes from numpy RandomState, operands from a counter hash on the GPU)",
         "config": {"workload": spec.name, "problems": spec.count, "cta": config_name,
-                   "path": "fma" if args.fma else "mfma", "best_sort_mode": row["mode"],
+                   "path": "fma" if args.fma else "mfma", "accumulate": "fp32", "best_sort_mode": row["mode"],
                    "gflop": round(flops / 1e9, 3), "algorithmic_gb": round(algo_bytes / 1e9, 4)},
         "mfma_peak_frac": round(mfma_frac, 4),
         "hbm_roofline_frac": round(hbm_frac, 4),

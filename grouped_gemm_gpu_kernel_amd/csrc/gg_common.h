@@ -202,11 +202,61 @@ __device__ __forceinline__ u32x4_t finish_piece(const RawPiece& r, uint32_t lead
 }
 
 // The loads of one stage in flight: this thread's A and B pieces.
+template <class G, bool WIDE>
+struct RawStage;
 template <class G>
-struct RawStage {
+struct RawStage<G, false> {
+  u32x4_t a[G::A_PER_THREAD];
+  u32x4_t b[G::B_PER_THREAD];
+};
+template <class G>
+struct RawStage<G, true> {
   RawPiece a[G::A_PER_THREAD];
   RawPiece b[G::B_PER_THREAD];
 };
+
+// Buffer resource over [base, base + bytes) for raw (unstrided) loads; bytes
+// is clamped to 2^32 - 1.  Loads of dwords outside the range return 0 without
+// touching memory, dword by dword (a 16-byte load that straddles the end
+// returns its in-range dwords), and a 16-byte load from a 2-byte aligned
+// offset returns the bytes at that offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  const int64_t n = bytes < 0 ? 0 : (bytes > 0xffffffffll ? 0xffffffffll : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(uint32_t)n, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
+// Replaces binary16 value idx of a 16-byte piece with h (low 16 bits); an idx
+// outside 0..7 leaves the piece unchanged.
+__device__ __forceinline__ u32x4_t put_value(u32x4_t v, int idx, uint32_t h) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w[j] = idx == 2 * j ? (w[j] & 0xffff0000u) | h : w[j];
+    w[j] = idx == 2 * j + 1 ? (w[j] & 0xffffu) | (h << 16) : w[j];
+  }
+  return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+// The binary16 value at p, read through the aligned dword that holds it
+// (wave-uniform address: a scalar load).
+__device__ __forceinline__ uint32_t load_value_uniform(const uint16_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t w = *(const __attribute__((address_space(4))) uint32_t*)(a & ~uintptr_t(3));
+  return (a & 2) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Keeps the first n (0..8) binary16 values of a 16-byte piece, zeroes the rest.
+__device__ __forceinline__ u32x4_t keep_values(u32x4_t v, int n) {
+  v.x &= n >= 2 ? 0xffffffffu : (n == 1 ? 0xffffu : 0u);
+  v.y &= n >= 4 ? 0xffffffffu : (n == 3 ? 0xffffu : 0u);
+  v.z &= n >= 6 ? 0xffffffffu : (n == 5 ? 0xffffu : 0u);
+  v.w &= n >= 8 ? 0xffffffffu : (n == 7 ? 0xffffu : 0u);
+  return v;
+}
 
 // Moves the A and B stages of one work tile from global memory into LDS.
 //
@@ -216,98 +266,121 @@ struct RawStage {
 //
 // Which values must be exact: D[i][j] depends only on row i of A and column j
 // of B, so rows of A past M and columns of B past N only reach elements of D
-// that are never stored.  Pieces that start past M or N are therefore not
-// loaded at all (their LDS slots receive zeros), and a B piece that straddles
-// N may bring in whatever follows column N - 1 in memory.  Values at k >= K
-// meet each other in the products, so a stage that reaches past K zero-fills
-// both operands.
+// that are never stored and may hold anything.  Values at k >= K meet each
+// other in the products, so both operands are zeroed there.
 //
-// Addressing (WIDE = false): the stage's origin is a wave-uniform byte address
-// (advanced with scalar arithmetic) and each piece has a fixed 32-bit byte
-// offset from it, set up once per tile; the host selects this form when
-// BM * lda and BK * ldb are below 2^30 and both are non-negative.  Inside
-// stages fetch a piece as 16 bytes plus, when it starts 2 bytes past a dword,
-// one more dword.  Inside means: for A, all k of the stage below K; for B, the
-// same, and when the tile's columns run past N also no row K - 1 in the stage
-// and ldb >= 8 -- a straddling piece then reads at most 18 bytes past its
-// row's last value, which lie in the next row, never past the matrix.  Other
-// stages fetch only the dwords that hold wanted values (same offsets).
-// WIDE = true computes 64-bit addresses per piece and uses that careful
-// fetch everywhere.
+// WIDE = false: every piece is one 16-byte buffer load at its exact byte
+// offset (2-byte aligned rows need no realignment), through a buffer resource
+// that spans from the tile's origin to the end of the matrix: rows of A past
+// M and rows of B past K lie beyond it (for ld >= the row length) and read as
+// zero without touching memory, and nothing past the matrix is ever read.  A
+// values at k >= K (the next row's head) and B rows at k >= K are zeroed when
+// the stage is written.  Every stage issues the same loads, with no branch,
+// so the compiler can count the loads in flight exactly.  The host selects
+// this form when the per-tile byte offsets fit in 31 bits
+// (rows * lda < 2^30, stage_k * ldb < 2^30, non-negative ld).  The range check
+// works on the access's dwords: when a piece starts 2 bytes past a dword, the
+// dword that holds the matrix's last value reaches 2 bytes past the matrix
+// and reads as 0, so the last value of A and of B is read separately (through
+// its aligned dword) and put back when the last stage is written.
+//
+// WIDE = true: 64-bit addresses per piece; each piece is fetched as the
+// dwords from the 4-byte aligned address at or below it that hold wanted
+// values (a dword past them is fetched from the first one again) and shifted
+// into place when written; values outside the matrix are zero-filled.
 template <class G, bool WIDE>
-struct StageLoader {
+struct StageLoader;
+
+template <class G>
+struct StageLoader<G, false> {
   static constexpr int T = G::THREADS;
   static constexpr int NA = G::A_PER_THREAD;
   static constexpr int NB = G::B_PER_THREAD;
   static constexpr int APR = G::BK / 8;  // A pieces per row
   static constexpr int BPR = G::BN / 8;  // B pieces per k-row
-  // A thread's pieces lie an even number of rows apart, so they share the
-  // 2-byte misalignment (lead) of their first piece.
-  static_assert((T / APR) % 2 == 0 && (T / BPR) % 2 == 0, "pieces of a thread must be an even number of rows apart");
-  static_assert(NA <= 32 && NB <= 32, "one live bit per piece");
+
+  const gg_device_problem_desc& p;
+  int tid;
+  __amdgpu_buffer_rsrc_t a_rsrc;  // A from (m0, 0) to the matrix end
+  const uint16_t* b_tile;         // B at (0, n0)
+  int64_t b_bytes;                // bytes from b_tile to the end of B
+  uint32_t a_off, b_off;          // byte offset of piece 0 from its origin
+  uint32_t a_step, b_step;        // byte distance between a thread's pieces
+  int m0, n0;
+  int last_stage;                 // index of the stage that holds k = K - 1
+  uint32_t a_last, b_last;        // A[m-1][k-1] and B[k-1][n-1]
+
+  __device__ __forceinline__ StageLoader(const gg_device_problem_desc& prob, int m0_, int n0_)
+      : p(prob), tid(opaque_tid()), m0(m0_), n0(n0_) {
+    const uint16_t* A = static_cast<const uint16_t*>(p.a);
+    const uint16_t* B = static_cast<const uint16_t*>(p.b);
+    const uint16_t* a_tile = A + (int64_t)m0 * p.lda;
+    // Last element of A is (m - 1, k - 1); of B, (k - 1, n - 1).
+    a_rsrc = buffer_rsrc(a_tile, 2 * ((int64_t)(p.m - 1 - m0) * p.lda + p.k));
+    b_tile = B + n0;
+    b_bytes = 2 * ((int64_t)(p.k - 1) * p.ldb + p.n - n0);
+    a_off = 2u * ((uint32_t)(tid / APR) * (uint32_t)p.lda + (uint32_t)(8 * (tid % APR)));
+    b_off = 2u * ((uint32_t)(tid / BPR) * (uint32_t)p.ldb + (uint32_t)(8 * (tid % BPR)));
+    a_step = 2u * (uint32_t)(T / APR) * (uint32_t)p.lda;
+    b_step = 2u * (uint32_t)(T / BPR) * (uint32_t)p.ldb;
+    last_stage = (p.k - 1) / G::BK;
+    a_last = p.k > 0 ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
+    b_last = p.k > 0 ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
+  }
+
+  // Issues the loads of stage kt into r.
+  __device__ __forceinline__ void issue(int kt, RawStage<G, false>& r) const {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) r.a[i] = buffer_load16(a_rsrc, a_off + i * a_step, 2u * G::BK * (uint32_t)kt);
+    const int64_t skip = 2 * (int64_t)G::BK * kt * p.ldb;
+    const __amdgpu_buffer_rsrc_t b_rsrc = buffer_rsrc(b_tile + skip / 2, b_bytes - skip);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) r.b[i] = buffer_load16(b_rsrc, b_off + i * b_step, 0u);
+  }
+
+  // Writes stage kt, fetched into r, into LDS buffer s (16-byte stores).
+  __device__ __forceinline__ void store(const RawStage<G, false>& r, int kt, uint16_t* lds, int s) const {
+    const int t = opaque_tid();
+    uint16_t* as = lds + s * G::STAGE;
+    uint16_t* bs = as + G::A_STAGE;
+    // A: a thread's pieces share their columns.
+    const int a_col = kt * G::BK + 8 * (t % APR);
+    const int a_keep = p.k - a_col;
+    const bool last = kt == last_stage;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int v = t + i * T;
+      u32x4_t val = keep_values(r.a[i], a_keep);
+      if (last) val = put_value(val, m0 + v / APR == p.m - 1 ? p.k - 1 - a_col : -1, a_last);
+      *reinterpret_cast<u32x4_t*>(as + (v / APR) * G::SA + 8 * (v % APR)) = val;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int v = t + i * T;
+      const int krow = kt * G::BK + v / BPR;
+      const u32x4_t zero = {0u, 0u, 0u, 0u};
+      u32x4_t val = krow < p.k ? r.b[i] : zero;
+      if (last) val = put_value(val, krow == p.k - 1 ? p.n - 1 - (n0 + 8 * (v % BPR)) : -1, b_last);
+      *reinterpret_cast<u32x4_t*>(bs + G::b_chunk(v / BPR, 8 * (v % BPR))) = val;
+    }
+  }
+};
+
+template <class G>
+struct StageLoader<G, true> {
+  static constexpr int T = G::THREADS;
+  static constexpr int NA = G::A_PER_THREAD;
+  static constexpr int NB = G::B_PER_THREAD;
+  static constexpr int APR = G::BK / 8;
+  static constexpr int BPR = G::BN / 8;
 
   const gg_device_problem_desc& p;
   int tid;
   int m0, n0;
-  bool b_inside;           // the tile's columns all lie below N
-  bool b_straddle_ok;      // b_inside, or ldb >= 8 (see above)
-  uintptr_t a_base0;       // 4-byte aligned origin of stage 0; stage kt adds 2*BK*kt bytes
-  uintptr_t b_base0;       // stage kt adds 2*BK*ldb*kt bytes
-  // Piece i lies i * (THREADS / APR) rows (A) or i * (THREADS / BPR) k-rows (B)
-  // below piece 0: its offset is off + i * step, with step wave-uniform.
-  uint32_t a_off, b_off;   // 4-byte aligned offset of piece 0 from the stage origin
-  uint32_t a_step, b_step; // byte distance between consecutive pieces of a thread
-  uint32_t a_live, b_live; // bit i: piece i starts below M (A) or below N (B)
-  uint32_t a_lead, b_lead; // 0 or 2: a thread's pieces share it
 
   __device__ __forceinline__ StageLoader(const gg_device_problem_desc& prob, int m0_, int n0_)
-      : p(prob), tid(opaque_tid()), m0(m0_), n0(n0_) {
-    b_inside = n0 + G::BN <= p.n;
-    b_straddle_ok = b_inside || p.ldb >= 8;
-    a_live = 0;
-    b_live = 0;
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      if (m0 + (tid + i * T) / APR < p.m) a_live |= 1u << i;
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      if (n0 + 8 * ((tid + i * T) % BPR) < p.n) b_live |= 1u << i;
-    }
-    if constexpr (!WIDE) {
-      const uintptr_t A = reinterpret_cast<uintptr_t>(p.a);
-      const uintptr_t B = reinterpret_cast<uintptr_t>(p.b);
-      a_base0 = (A & ~uintptr_t(3)) + (uintptr_t)((int64_t)m0 * p.lda * 2);
-      b_base0 = (B & ~uintptr_t(3)) + (uintptr_t)((int64_t)n0 * 2);
-      const uint32_t a_rel = (uint32_t)(tid / APR) * (uint32_t)p.lda * 2u + (uint32_t)(16 * (tid % APR)) + (uint32_t)(A & 3);
-      const uint32_t b_rel = (uint32_t)(tid / BPR) * (uint32_t)p.ldb * 2u + (uint32_t)(16 * (tid % BPR)) + (uint32_t)(B & 3);
-      a_off = a_rel & ~3u;
-      b_off = b_rel & ~3u;
-      a_lead = a_rel & 2u;
-      b_lead = b_rel & 2u;
-      a_step = (uint32_t)(T / APR) * (uint32_t)p.lda * 2u;
-      b_step = (uint32_t)(T / BPR) * (uint32_t)p.ldb * 2u;
-    }
-  }
+      : p(prob), tid(opaque_tid()), m0(m0_), n0(n0_) {}
 
-  __device__ __forceinline__ bool a_fast(int kt) const { return !WIDE && (kt + 1) * G::BK <= p.k; }
-  __device__ __forceinline__ bool b_fast(int kt) const {
-    return !WIDE && ((kt + 1) * G::BK < p.k ? b_straddle_ok : (b_inside && (kt + 1) * G::BK == p.k));
-  }
-
-  // Values of A piece i / B piece i of stage kt inside the matrix (0..8).
-  __device__ __forceinline__ uint32_t a_nvalid(int i, int kt) const {
-    const int v = tid + i * T;
-    const int n = p.k - (kt * G::BK + 8 * (v % APR));
-    return (a_live & (1u << i)) ? (uint32_t)(n < 0 ? 0 : (n > 8 ? 8 : n)) : 0u;
-  }
-  __device__ __forceinline__ uint32_t b_nvalid(int i, int kt) const {
-    const int v = tid + i * T;
-    const int n = p.n - (n0 + 8 * (v % BPR));
-    return ((b_live & (1u << i)) && kt * G::BK + v / BPR < p.k) ? (uint32_t)(n < 0 ? 0 : (n > 8 ? 8 : n)) : 0u;
-  }
-
-  // Placement of A piece i and B piece i of stage kt with 64-bit addresses (WIDE).
   __device__ __forceinline__ EdgePlace a_edge(int i, int kt) const {
     const int v = tid + i * T;
     return edge_place(static_cast<const uint16_t*>(p.a), p.lda, p.m, p.k, m0 + v / APR, kt * G::BK + 8 * (v % APR));
@@ -317,115 +390,28 @@ struct StageLoader {
     return edge_place(static_cast<const uint16_t*>(p.b), p.ldb, p.k, p.n, kt * G::BK + v / BPR, n0 + 8 * (v % BPR));
   }
 
-  // 16 bytes from off and, when the piece starts 2 bytes past off (lead 2),
-  // the dword after them, else the first dword again (the shift ignores it).
-  // Unconditional: a branch here costs more than the extra load.
-  static __device__ __forceinline__ void fetch(uintptr_t base, uint32_t off, uint32_t lead, RawPiece& out) {
-    const u32x4_t v = *(g_u32x4_t*)(base + off);
-    out.w[0] = v.x;
-    out.w[1] = v.y;
-    out.w[2] = v.z;
-    out.w[3] = v.w;
-    out.w[4] = *(g_u32_t*)(base + off + 8u * lead);
+  __device__ __forceinline__ void issue(int kt, RawStage<G, true>& r) const {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) issue_piece_edge(a_edge(i, kt), r.a[i]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) issue_piece_edge(b_edge(i, kt), r.b[i]);
   }
 
-  // Fetches only the dwords of a piece that hold one of its nvalid values; a
-  // dword past them is fetched from off itself (a wanted dword).
-  static __device__ __forceinline__ void fetch_careful(uintptr_t base, uint32_t off, uint32_t lead, uint32_t nvalid,
-                                                       RawPiece& out) {
-    if (nvalid == 0) {
-      skip_piece(out);
-      return;
-    }
-    const uint32_t span = lead + 2u * nvalid;
-#pragma unroll
-    for (int j = 0; j < 5; ++j) out.w[j] = *(g_u32_t*)(base + ((4u * j < span) ? off + 4u * j : off));
-  }
-
-  __device__ __forceinline__ uintptr_t a_stage_base(int kt) const {
-    return a_base0 + (uintptr_t)(2 * G::BK) * (uintptr_t)kt;
-  }
-  __device__ __forceinline__ uintptr_t b_stage_base(int kt) const {
-    return b_base0 + (uintptr_t)((int64_t)2 * G::BK * p.ldb) * (uintptr_t)kt;
-  }
-
-  // Issues the loads of stage kt into r.
-  __device__ __forceinline__ void issue(int kt, RawStage<G>& r) const {
-    if constexpr (WIDE) {
-#pragma unroll
-      for (int i = 0; i < NA; ++i) issue_piece_edge(a_edge(i, kt), r.a[i]);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) issue_piece_edge(b_edge(i, kt), r.b[i]);
-    } else {
-      const uintptr_t abase = a_stage_base(kt);
-      if (a_fast(kt)) {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-          if (a_live & (1u << i)) {
-            fetch(abase, a_off + i * a_step, a_lead, r.a[i]);
-          } else {
-            skip_piece(r.a[i]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) fetch_careful(abase, a_off + i * a_step, a_lead, a_nvalid(i, kt), r.a[i]);
-      }
-      const uintptr_t bbase = b_stage_base(kt);
-      if (b_fast(kt)) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          if (b_live & (1u << i)) {
-            fetch(bbase, b_off + i * b_step, b_lead, r.b[i]);
-          } else {
-            skip_piece(r.b[i]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) fetch_careful(bbase, b_off + i * b_step, b_lead, b_nvalid(i, kt), r.b[i]);
-      }
-    }
-  }
-
-  // Shifts a piece fetched by `fetch` into place.
-  static __device__ __forceinline__ u32x4_t shift_fast(const RawPiece& r, uint32_t lead) {
-    u32x4_t out;
-    out.x = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], lead);
-    out.y = __builtin_amdgcn_alignbyte(r.w[2], r.w[1], lead);
-    out.z = __builtin_amdgcn_alignbyte(r.w[3], r.w[2], lead);
-    out.w = __builtin_amdgcn_alignbyte(r.w[4], r.w[3], lead);
-    return out;
-  }
-
-  // Writes stage kt, fetched into r, into LDS buffer s (16-byte stores).
-  __device__ __forceinline__ void store(const RawStage<G>& r, int kt, uint16_t* lds, int s) const {
-    const int tid = opaque_tid();
+  __device__ __forceinline__ void store(const RawStage<G, true>& r, int kt, uint16_t* lds, int s) const {
+    const int t = opaque_tid();
     uint16_t* as = lds + s * G::STAGE;
     uint16_t* bs = as + G::A_STAGE;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      const int v = tid + i * T;
-      u32x4_t val;
-      if constexpr (WIDE) {
-        const EdgePlace e = a_edge(i, kt);
-        val = finish_piece(r.a[i], e.lead, e.nvalid);
-      } else {
-        val = a_fast(kt) ? shift_fast(r.a[i], a_lead) : finish_piece(r.a[i], a_lead, a_nvalid(i, kt));
-      }
-      *reinterpret_cast<u32x4_t*>(as + (v / APR) * G::SA + 8 * (v % APR)) = val;
+      const int v = t + i * T;
+      const EdgePlace e = a_edge(i, kt);
+      *reinterpret_cast<u32x4_t*>(as + (v / APR) * G::SA + 8 * (v % APR)) = finish_piece(r.a[i], e.lead, e.nvalid);
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int v = tid + i * T;
-      u32x4_t val;
-      if constexpr (WIDE) {
-        const EdgePlace e = b_edge(i, kt);
-        val = finish_piece(r.b[i], e.lead, e.nvalid);
-      } else {
-        val = b_fast(kt) ? shift_fast(r.b[i], b_lead) : finish_piece(r.b[i], b_lead, b_nvalid(i, kt));
-      }
-      *reinterpret_cast<u32x4_t*>(bs + G::b_chunk(v / BPR, 8 * (v % BPR))) = val;
+      const int v = t + i * T;
+      const EdgePlace e = b_edge(i, kt);
+      *reinterpret_cast<u32x4_t*>(bs + G::b_chunk(v / BPR, 8 * (v % BPR))) = finish_piece(r.b[i], e.lead, e.nvalid);
     }
   }
 };

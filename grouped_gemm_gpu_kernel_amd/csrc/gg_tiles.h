@@ -27,7 +27,7 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
   const int nk = (p.k + G::BK - 1) / G::BK;
   if (nk <= 0) return;
   const StageLoader<G, WIDE> loader(p, m0, n0);
-  RawStage<G> ring[D];
+  RawStage<G, WIDE> ring[D];
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) {
     if (s < nk) loader.issue(s, ring[s]);

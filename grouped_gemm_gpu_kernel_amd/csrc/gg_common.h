@@ -298,20 +298,26 @@ struct StageLoader<G, false> {
   static constexpr int NB = G::B_PER_THREAD;
   static constexpr int APR = G::BK / 8;  // A pieces per row
   static constexpr int BPR = G::BN / 8;  // B pieces per k-row
+  // LDS distance between a thread's consecutive pieces.  The B swizzle
+  // repeats every 4 k-rows, so it is the same for all of a thread's pieces.
+  static constexpr int A_LDS_STEP = (T / APR) * G::SA;
+  static constexpr int B_LDS_STEP = (T / BPR) * G::SB;
+  static_assert((T / BPR) % 4 == 0, "a thread's B pieces must share their swizzle");
 
   const gg_device_problem_desc& p;
-  int tid;
   __amdgpu_buffer_rsrc_t a_rsrc;  // A from (m0, 0) to the matrix end
   const uint16_t* b_tile;         // B at (0, n0)
   int64_t b_bytes;                // bytes from b_tile to the end of B
-  uint32_t a_off, b_off;          // byte offset of piece 0 from its origin
-  uint32_t a_step, b_step;        // byte distance between a thread's pieces
+  uint32_t a_off, b_off;          // byte offset of this thread's piece 0 from its origin
+  uint32_t a_step, b_step;        // byte distance between a thread's pieces (wave-uniform)
+  int a_lds, b_lds;               // LDS offset (values) of piece 0 within a stage's A / B part
   int m0, n0;
   int last_stage;                 // index of the stage that holds k = K - 1
   uint32_t a_last, b_last;        // A[m-1][k-1] and B[k-1][n-1]
 
   __device__ __forceinline__ StageLoader(const gg_device_problem_desc& prob, int m0_, int n0_)
-      : p(prob), tid(opaque_tid()), m0(m0_), n0(n0_) {
+      : p(prob), m0(m0_), n0(n0_) {
+    const int tid = opaque_tid();
     const uint16_t* A = static_cast<const uint16_t*>(p.a);
     const uint16_t* B = static_cast<const uint16_t*>(p.b);
     const uint16_t* a_tile = A + (int64_t)m0 * p.lda;
@@ -323,45 +329,54 @@ struct StageLoader<G, false> {
     b_off = 2u * ((uint32_t)(tid / BPR) * (uint32_t)p.ldb + (uint32_t)(8 * (tid % BPR)));
     a_step = 2u * (uint32_t)(T / APR) * (uint32_t)p.lda;
     b_step = 2u * (uint32_t)(T / BPR) * (uint32_t)p.ldb;
+    a_lds = (tid / APR) * G::SA + 8 * (tid % APR);
+    b_lds = G::b_chunk(tid / BPR, 8 * (tid % BPR));
     last_stage = (p.k - 1) / G::BK;
     a_last = p.k > 0 ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
     b_last = p.k > 0 ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
   }
 
-  // Issues the loads of stage kt into r.
+  // Issues the loads of stage kt into r.  The per-piece and per-stage parts of
+  // the offsets are wave-uniform (scalar offset operand).
   __device__ __forceinline__ void issue(int kt, RawStage<G, false>& r) const {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) r.a[i] = buffer_load16(a_rsrc, a_off + i * a_step, 2u * G::BK * (uint32_t)kt);
+    for (int i = 0; i < NA; ++i) r.a[i] = buffer_load16(a_rsrc, a_off, 2u * G::BK * (uint32_t)kt + i * a_step);
     const int64_t skip = 2 * (int64_t)G::BK * kt * p.ldb;
     const __amdgpu_buffer_rsrc_t b_rsrc = buffer_rsrc(b_tile + skip / 2, b_bytes - skip);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) r.b[i] = buffer_load16(b_rsrc, b_off + i * b_step, 0u);
+    for (int i = 0; i < NB; ++i) r.b[i] = buffer_load16(b_rsrc, b_off, i * b_step);
   }
 
-  // Writes stage kt, fetched into r, into LDS buffer s (16-byte stores).
+  // Writes stage kt, fetched into r, into LDS buffer s (16-byte stores).  Only
+  // the stage that holds k = K - 1 needs masking: A values at k >= K (the next
+  // row's head), B rows at k >= K, and the matrices' last values.
   __device__ __forceinline__ void store(const RawStage<G, false>& r, int kt, uint16_t* lds, int s) const {
+    uint16_t* as = lds + s * G::STAGE + a_lds;
+    uint16_t* bs = lds + s * G::STAGE + G::A_STAGE + b_lds;
+    if (kt != last_stage) {
+#pragma unroll
+      for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4_t*>(as + i * A_LDS_STEP) = r.a[i];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) *reinterpret_cast<u32x4_t*>(bs + i * B_LDS_STEP) = r.b[i];
+      return;
+    }
     const int t = opaque_tid();
-    uint16_t* as = lds + s * G::STAGE;
-    uint16_t* bs = as + G::A_STAGE;
-    // A: a thread's pieces share their columns.
-    const int a_col = kt * G::BK + 8 * (t % APR);
-    const int a_keep = p.k - a_col;
-    const bool last = kt == last_stage;
+    const int a_col = kt * G::BK + 8 * (t % APR);  // a thread's pieces share their columns
+    const int a_row = m0 + t / APR;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      const int v = t + i * T;
-      u32x4_t val = keep_values(r.a[i], a_keep);
-      if (last) val = put_value(val, m0 + v / APR == p.m - 1 ? p.k - 1 - a_col : -1, a_last);
-      *reinterpret_cast<u32x4_t*>(as + (v / APR) * G::SA + 8 * (v % APR)) = val;
+      u32x4_t val = keep_values(r.a[i], p.k - a_col);
+      val = put_value(val, a_row + i * (T / APR) == p.m - 1 ? p.k - 1 - a_col : -1, a_last);
+      *reinterpret_cast<u32x4_t*>(as + i * A_LDS_STEP) = val;
     }
+    const int b_col = n0 + 8 * (t % BPR);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int v = t + i * T;
-      const int krow = kt * G::BK + v / BPR;
+      const int krow = kt * G::BK + t / BPR + i * (T / BPR);
       const u32x4_t zero = {0u, 0u, 0u, 0u};
       u32x4_t val = krow < p.k ? r.b[i] : zero;
-      if (last) val = put_value(val, krow == p.k - 1 ? p.n - 1 - (n0 + 8 * (v % BPR)) : -1, b_last);
-      *reinterpret_cast<u32x4_t*>(bs + G::b_chunk(v / BPR, 8 * (v % BPR))) = val;
+      val = put_value(val, krow == p.k - 1 ? p.n - 1 - b_col : -1, b_last);
+      *reinterpret_cast<u32x4_t*>(bs + i * B_LDS_STEP) = val;
     }
   }
 };

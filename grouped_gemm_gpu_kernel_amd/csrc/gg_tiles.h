@@ -166,9 +166,13 @@ struct MfmaTile {
   // the block for lane (h, c) = (lane / 32, lane % 32).  A 4 x 4 transpose in
   // each quad of lanes (c = 4j .. 4j+3) gives lane (h, 4j + q) row 8g + 4h + q,
   // columns 4j .. 4j+3, so C is read and D written as 16-byte vectors: a
-  // dword access costs the address unit as much as a 16-byte one.  Columns
-  // that cross N go element by element.  With 32-bit addressing each access
-  // is a wave-uniform 64-bit row origin plus a per-lane 32-bit offset.
+  // dword access costs the address unit as much as a 16-byte one.
+  //
+  // With 32-bit addressing all C vectors of the block are requested before
+  // any is used, through a buffer resource from (r0, c0) to the end of C:
+  // rows past M read as zero, so the loads need no branch and their latencies
+  // overlap.  Stores go through the same kind of resource; columns that cross
+  // N go element by element.
   template <bool WIDE>
   __device__ __forceinline__ static void store_tile(const gg_device_problem_desc& p, int r0, int c0, int lane,
                                                     const floatx16_t (&acc)[FM][FN]) {
@@ -176,41 +180,76 @@ struct MfmaTile {
     const int q = lane & 3;
     const int lrow = 4 * (lane >> 5) + q;  // row within an 8-row group
     const int lcol = (lane & 31) & ~3;     // first column of the lane's vector
+    if constexpr (!WIDE) {
+      floatx4_t cv[FM][FN][4];
+      if (use_c) {
+        const __amdgpu_buffer_rsrc_t crs =
+            buffer_rsrc(p.c + ((int64_t)r0 * p.ldc + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldc + (p.n - c0)));
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
+        for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int col = c0 + fn * 32 + lcol;
-        const int ncol = p.n - col;  // columns of the vector inside the matrix
+          for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                        acc[fm][fn][4 * g + 3]};
-          quad_transpose(v, q);
-          const int urow = r0 + fm * 32 + 8 * g;  // wave-uniform
-          const int row = urow + lrow;
-          if (row >= p.m || ncol <= 0) continue;
-          g_cf32_t* crow;
-          g_f32_t* drow;
-          if constexpr (WIDE) {
-            crow = (g_cf32_t*)p.c + ((int64_t)row * p.ldc + col);
-            drow = (g_f32_t*)p.d + ((int64_t)row * p.ldd + col);
-          } else {
-            crow = (g_cf32_t*)p.c + ((int64_t)urow * p.ldc + c0) + (uint32_t)(lrow * p.ldc + fn * 32 + lcol);
-            drow = (g_f32_t*)p.d + ((int64_t)urow * p.ldd + c0) + (uint32_t)(lrow * p.ldd + fn * 32 + lcol);
-          }
-          if (ncol >= 4) {
-            floatx4_t cv = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (use_c) cv = *(const __attribute__((address_space(1))) floatx4_t*)crow;
+            for (int g = 0; g < 4; ++g) {
+              const uint32_t off = 4u * ((uint32_t)(fm * 32 + 8 * g + lrow) * (uint32_t)p.ldc + fn * 32 + lcol);
+              cv[fm][fn][g] = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(crs, (int)off, 0, 0));
+            }
+      } else {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) cv[fm][fn][g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      const __amdgpu_buffer_rsrc_t drs =
+          buffer_rsrc(p.d + ((int64_t)r0 * p.ldd + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldd + (p.n - c0)));
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int ncol = p.n - (c0 + fn * 32 + lcol);  // columns of the vector inside the matrix
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                          acc[fm][fn][4 * g + 3]};
+            quad_transpose(v, q);
+            const int rrow = fm * 32 + 8 * g + lrow;
             floatx4_t out;
-            out[0] = epilogue_value(v[0], cv[0], p.alpha, p.beta);
-            out[1] = epilogue_value(v[1], cv[1], p.alpha, p.beta);
-            out[2] = epilogue_value(v[2], cv[2], p.alpha, p.beta);
-            out[3] = epilogue_value(v[3], cv[3], p.alpha, p.beta);
-            *(__attribute__((address_space(1))) floatx4_t*)drow = out;
-          } else {
 #pragma unroll
-            for (int e = 0; e < 3; ++e) {
+            for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[fm][fn][g][e], p.alpha, p.beta);
+            if (r0 + rrow >= p.m || ncol <= 0) continue;
+            const uint32_t off = 4u * ((uint32_t)rrow * (uint32_t)p.ldd + fn * 32 + lcol);
+            if (ncol >= 4) {
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) int, out),
+                                                     drs, (int)off, 0, 0);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 3; ++e) {
+                if (e < ncol) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(out[e]), drs, (int)(off + 4 * e), 0, 0);
+              }
+            }
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int col = c0 + fn * 32 + lcol;
+          const int ncol = p.n - col;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                          acc[fm][fn][4 * g + 3]};
+            quad_transpose(v, q);
+            const int row = r0 + fm * 32 + 8 * g + lrow;
+            if (row >= p.m || ncol <= 0) continue;
+            g_cf32_t* crow = (g_cf32_t*)p.c + ((int64_t)row * p.ldc + col);
+            g_f32_t* drow = (g_f32_t*)p.d + ((int64_t)row * p.ldd + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
               if (e < ncol) drow[e] = epilogue_value(v[e], use_c ? crow[e] : 0.0f, p.alpha, p.beta);
             }
           }

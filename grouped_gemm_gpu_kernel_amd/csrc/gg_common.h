@@ -85,7 +85,7 @@ struct Geometry {
 #define GG_STAGE_K 64
 #endif
 #ifndef GG_STAGE_DEPTH
-#define GG_STAGE_DEPTH 2
+#define GG_STAGE_DEPTH 3
 #endif
 
 // Reference macro-tile of each variant (ids follow GGK_VARIANT_*).

@@ -18,8 +18,14 @@ namespace gg {
 // Stage s is fetched into register set s % DEPTH.  While stage k is
 // multiplied out of LDS buffer k % 2, the loads of stage k + DEPTH - 1 are
 // issued and stage k + 1 (issued DEPTH - 1 stages earlier) is written to the
-// other LDS buffer; one barrier closes the step.  The loop body is unrolled
-// DEPTH times so that every register set is addressed statically.
+// other LDS buffer; one barrier closes the step.  Loads and LDS writes are
+// issued for every step, also for stages past K (which read as zero without
+// touching memory and land in a buffer nobody reads): a load under a branch
+// would make the compiler wait for every load in flight before the next LDS
+// write, and only DEPTH - 1 = 1 stage could ever be in flight.  The main loop
+// runs whole groups of DEPTH steps with no branch; the last steps of a tile
+// are guarded.  The body is unrolled DEPTH times so that every register set
+// is addressed statically.
 template <class G, bool WIDE, class Compute>
 __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
                                            Compute&& compute) {
@@ -29,22 +35,23 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
   const StageLoader<G, WIDE> loader(p, m0, n0);
   RawStage<G, WIDE> ring[D];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) {
-    if (s < nk) loader.issue(s, ring[s]);
-  }
+  for (int s = 0; s < D - 1; ++s) loader.issue(s, ring[s]);
   loader.store(ring[0], 0, lds, 0);
   __syncthreads();
-  for (int k0 = 0; k0 < nk; k0 += D) {
+  auto step = [&](int k, int u) {
+    loader.issue(k + D - 1, ring[(u + D - 1) % D]);
+    compute(lds + (k & 1) * G::STAGE);
+    loader.store(ring[(u + 1) % D], k + 1, lds, (k + 1) & 1);
+    __syncthreads();
+  };
+  int k0 = 0;
+  for (; k0 + D <= nk; k0 += D) {
 #pragma unroll
-    for (int u = 0; u < D; ++u) {
-      const int k = k0 + u;
-      if (k < nk) {
-        if (k + D - 1 < nk) loader.issue(k + D - 1, ring[(u + D - 1) % D]);
-        compute(lds + (k & 1) * G::STAGE);
-        if (k + 1 < nk) loader.store(ring[(u + 1) % D], k + 1, lds, (k + 1) & 1);
-        __syncthreads();
-      }
-    }
+    for (int u = 0; u < D; ++u) step(k0 + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u < D - 1; ++u) {
+    if (k0 + u < nk) step(k0 + u, u);
   }
 }
 

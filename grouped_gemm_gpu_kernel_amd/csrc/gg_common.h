@@ -100,9 +100,15 @@ template <> struct VariantTile<GGK_VARIANT_64x128x32> { static constexpr int M =
 // single reference tile, which halves the L2 -> CU traffic that bounds these
 // kernels.  The FMA path computes one reference tile with 256 threads.
 template <int V, int PATH> struct KernelShape;
+#ifndef GG_WORK_TM
+#define GG_WORK_TM 2
+#endif
+#ifndef GG_WORK_TN
+#define GG_WORK_TN 2
+#endif
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
-  static constexpr int TM = 2;  // reference tiles per work tile, along M
-  static constexpr int TN = 2;  // and along N
+  static constexpr int TM = GG_WORK_TM;  // reference tiles per work tile, along M
+  static constexpr int TN = GG_WORK_TN;  // and along N
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
   using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, (BM / 64) * (BN / 64) * kWave>;

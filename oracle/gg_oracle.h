@@ -49,9 +49,16 @@ int go_uniform_int(go_mt19937* mt, int lo, int hi);
 float go_uniform_real_f32(go_mt19937* mt, float lo, float hi);
 
 /* Shapes of the reference benchmark's workloads "small", "tail", "mixed"
- * (bench/benchmark_grouped_gemm.cu:368-443).  Returns 0, or -1 for an unknown
- * workload name. */
+ * (bench/benchmark_grouped_gemm.cu:368-443), picks drawn k, n, m as the
+ * reference binary draws them.  Returns 0, or -1 for an unknown workload name. */
 int go_bench_shapes(const char* workload, int count, uint32_t seed, int* m, int* n, int* k);
+
+/* The "small"/"mixed" recipe over caller-given candidate lists: per problem a
+ * uniform pick for k, then n, then m.  Lets the published rows made with the
+ * reference's earlier mixed lists (bench/benchmark_grouped_gemm.cu:409-411,
+ * now commented out) be regenerated. */
+void go_bench_shapes_lists(int count, uint32_t seed, const int* mv, int mc, const int* nv, int nc, const int* kv,
+                           int kc, int* m, int* n, int* k);
 
 /* The reference test's inputs (tests/test_correctness.cu:106-150): for each
  * shape draws alpha, beta, then A (m x max(1,k)), B (k x max(1,n)),

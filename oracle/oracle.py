@@ -39,6 +39,7 @@ _SIGS = {
     "go_uniform_int": (_i, [ctypes.POINTER(MT19937), _i, _i]),
     "go_uniform_real_f32": (ctypes.c_float, [ctypes.POINTER(MT19937), ctypes.c_float, ctypes.c_float]),
     "go_bench_shapes": (_i, [ctypes.c_char_p, _i, ctypes.c_uint32, _ip, _ip, _ip]),
+    "go_bench_shapes_lists": (None, [_i, ctypes.c_uint32, _ip, _i, _ip, _i, _ip, _i, _ip, _ip, _ip]),
     "go_reference_test_inputs": (None, [_i, _ip, _ip, _ip, ctypes.c_uint32, _fp, _fp, _i64p, _i64p, _i64p,
                                         _u16p, _u16p, _fp]),
     "go_tile_count": (_i, [_i, _i, _i, _i]),
@@ -120,6 +121,15 @@ def bench_shapes(workload: str, count: int, seed: int):
     k = np.zeros(count, np.int32)
     if lib().go_bench_shapes(workload.encode(), count, seed, _p(m, _ip), _p(n, _ip), _p(k, _ip)) != 0:
         raise ValueError(workload)
+    return m, n, k
+
+
+def bench_shapes_lists(count: int, seed: int, m_values, n_values, k_values):
+    """The small/mixed recipe over given candidate lists (gg_oracle.h)."""
+    lists = [np.ascontiguousarray(v, np.int32) for v in (m_values, n_values, k_values)]
+    m, n, k = (np.zeros(count, np.int32) for _ in range(3))
+    lib().go_bench_shapes_lists(count, seed, _p(lists[0], _ip), lists[0].size, _p(lists[1], _ip), lists[1].size,
+                                _p(lists[2], _ip), lists[2].size, _p(m, _ip), _p(n, _ip), _p(k, _ip))
     return m, n, k
 
 

@@ -1,6 +1,9 @@
 """Host-side parity of the library, on the CPU: prepare_problem_set (sort permutations, tile offsets,
 total tiles), tile counts, sort-mode names and empty-problem counting must equal the oracle bit for
 bit.  These entry points never touch the GPU."""
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -58,16 +61,24 @@ def test_prepare_reference_shapes_and_bench_workloads():
                     O.tail_work_share(np.asarray(k)[perm], offs, cfg.cta_k), abs=0, rel=1e-15)
 
 
-def test_published_small_workload_through_library():
-    """bench/results_20260331/results.csv:2-15: tiles 300/300/256 and the sort_by_k tail shares."""
-    m, n, k = O.bench_shapes("small", 256, 42)
-    probs = _problems(m, n, k)
-    for config, tiles, share in (("64x64x16", 300, 0.035), ("128x64x32", 300, 0.061), ("64x128x32", 256, None)):
-        cfg = KernelConfig.named(config)
-        prep = api.prepare_problem_set(probs, cfg, SortMode.kByK)
-        assert prep.total_tiles == tiles
-        if share is not None:
-            assert round(api.tail_work_share(prep, cfg), 3) == share
+def test_published_rows_through_library():
+    """bench/results_20260331/results.csv, the 256-problem seed-42 rows of the small and tail
+    workloads: the library's prepare gives the published tile totals and tail shares in every mode."""
+    rows = json.loads((Path(__file__).resolve().parent / "golden" / "published_bench_rows.json").read_text())["rows"]
+    checked = 0
+    for row in rows:
+        if row["workload"] == "mixed" or row["problems"] != 256 or row["seed"] != 42:
+            continue
+        if row["mode"] == "baseline_per_problem" or row["persistent_ctas"]:
+            continue
+        m, n, k = O.bench_shapes(row["workload"], 256, 42)
+        cfg = KernelConfig.named(row["config"])
+        mode = next(md for md in SortMode if api.sort_mode_name(md) == row["mode"])
+        prep = api.prepare_problem_set(_problems(m, n, k), cfg, mode)
+        assert prep.total_tiles == row["tiles"], row
+        assert round(api.tail_work_share(prep, cfg), 3) == row["tail_share"], row
+        checked += 1
+    assert checked == 28  # 24 grid rows and a repeat of one tail row in the problem-count sweep
 
 
 def test_by_tiles_then_k_equals_by_tiles():

@@ -101,35 +101,75 @@ def _golden(name):
     return json.loads((GOLDEN / name).read_text())
 
 
-def test_published_small_workload_tile_totals_and_tail_shares():
-    """bench/results_20260331/results.csv:2-15 (small workload, 256 problems, seed 42): tile totals
-    300/300/256 per macro-tile, and sort_by_k tail shares 0.035 (64x64x16), 0.061 (128x64x32) under the
-    current tail definition max(1, P/10) (bench/benchmark_grouped_gemm.cu:586)."""
-    g = _golden("published_small_seed42.json")
-    m, n, k = O.bench_shapes("small", g["problems"], g["seed"])
-    for row in g["rows"]:
-        cm, cn, ck = row["cta"]
-        perm, offs, total = O.prepare(m, n, k, cm, cn, 1)
+# The reference's mixed rows were published with its earlier mixed candidate lists, now commented
+# out (bench/benchmark_grouped_gemm.cu:409-411); small and tail rows use the current generators.
+LEGACY_MIXED = ([16, 24, 32, 48, 64, 96, 128, 160], [16, 32, 48, 64, 96, 128, 192],
+                [16, 24, 32, 48, 64, 96, 128, 192, 256])
+MODES = {"none": 0, "sort_by_k": 1, "sort_by_tiles": 2, "sort_by_tiles_then_k": 3}
+
+
+def published_shapes(row):
+    if row["workload"] == "mixed":
+        return O.bench_shapes_lists(row["problems"], row["seed"], *LEGACY_MIXED)
+    return O.bench_shapes(row["workload"], row["problems"], row["seed"])
+
+
+def test_published_rows_tile_totals_and_tail_shares():
+    """Every grouped row of bench/results_20260331/results.csv (3 workloads x 3 macro-tiles, problem
+    counts 64..1024, five seeds, persistent grids): the oracle's shapes and sort permutations give the
+    published tile total and, with the tail counted as max(1, P/10) problems
+    (bench/benchmark_grouped_gemm.cu:586), the published tail share of every sort mode.  The tail
+    rows fix the generators' draw order (k, then n, then m); the by-tiles rows fix the by-tiles
+    order (ties broken by k, then m*n)."""
+    rows = _golden("published_bench_rows.json")["rows"]
+    checked = 0
+    for row in rows:
+        if row["mode"] == "baseline_per_problem":
+            continue
+        m, n, k = published_shapes(row)
+        cm, cn, ck = (int(x) for x in row["config"].split("x"))
+        perm, offs, total = O.prepare(m, n, k, cm, cn, MODES[row["mode"]])
         assert total == row["tiles"], row
-        if row["config"] in ("64x64x16", "128x64x32"):
-            share = O.tail_work_share(k[perm], offs, ck)
-            assert round(share, 3) == row["tail_share"]["sort_by_k"], row
+        assert round(O.tail_work_share(k[perm], offs, ck), 3) == row["tail_share"], row
+        if row["persistent_ctas"] > 0:
+            assert row["grid_ctas"] == row["persistent_ctas"], row
+        checked += 1
+    assert checked == 192
 
 
-def test_published_by_tiles_tail_shares_pin_sort_order():
-    """The published sort_by_tiles / sort_by_tiles_then_k tail shares (0.035, 0.061, 0.071) came from a
-    build that counted the tail as ceil(P/10) problems.  With that count, the oracle's by-tiles
-    permutations reproduce all six, which pins the by-tiles order (ties broken by k, then m*n)."""
-    g = _golden("published_small_seed42.json")
-    m, n, k = O.bench_shapes("small", g["problems"], g["seed"])
-    for row in g["rows"]:
-        cm, cn, ck = row["cta"]
-        for mode, key in ((2, "sort_by_tiles"), (3, "sort_by_tiles_then_k")):
-            perm, offs, _ = O.prepare(m, n, k, cm, cn, mode)
-            cnt = len(perm)
-            tail = max(1, -(-cnt // 10))
-            work = np.diff(offs).astype(np.float64) * ((k[perm] + ck - 1) // ck)
-            assert round(float(work[-tail:].sum() / work.sum()), 3) == row["tail_share"][key], (row, key)
+def test_published_rows_flops_and_launch_counts():
+    """TFLOP/s x kernel ms = total FLOPs / 1e9 for every published row; both figures are rounded to
+    three decimals, so the oracle's 2*m*n*k sum must fall inside the product of their rounding
+    intervals.  Baseline rows launch once per non-empty problem."""
+    rows = _golden("published_bench_rows.json")["rows"]
+    for row in rows:
+        m, n, k = published_shapes(row)
+        gflop = O.total_flops(m, n, k) / 1e9
+        t, ms = row["tflops"], row["kernel_ms"]
+        assert (t - 5e-4) * (ms - 5e-4) <= gflop <= (t + 5e-4) * (ms + 5e-4), row
+        if row["mode"] == "baseline_per_problem":
+            assert row["launches"] == int(((m > 0) & (n > 0)).sum()), row
+            assert row["tiles"] == O.prepare(m, n, k, *(int(x) for x in row["config"].split("x")[:2]), 0)[2]
+
+
+def test_shape_draw_order_is_pinned():
+    """The tail rows at 256 problems, seed 42 (630 / 447 / 444 tiles) hold only for the k, n, m draw
+    order; drawing m, n, k from the same stream gives other totals."""
+    m, n, k = O.bench_shapes("tail", 256, 42)
+    got = [int(O.prepare(m, n, k, cm, cn, 0)[2]) for cm, cn in ((64, 64), (128, 64), (64, 128))]
+    assert got == [630, 447, 444]
+    mt = O.Mt19937(42)
+    small_mn, large_mn = [16, 24, 32, 48, 64], [96, 128, 160, 192, 256]
+    small_k, large_k = [16, 24, 32, 48, 64], [96, 128, 192, 256, 384, 512]
+    mm, nn = [], []
+    for _ in range(256):
+        small = np.float32(mt.uniform_real(0.0, 1.0)) < np.float32(0.8)
+        lm, lk = (small_mn, small_k) if small else (large_mn, large_k)
+        mm.append(lm[mt.uniform_int(0, len(lm) - 1)])
+        nn.append(lm[mt.uniform_int(0, len(lm) - 1)])
+        mt.uniform_int(0, len(lk) - 1)
+    other = sum(-(-a // 64) * -(-b // 64) for a, b in zip(mm, nn))
+    assert other != 630
 
 
 # ---------------------------------------------------------------- prepare path

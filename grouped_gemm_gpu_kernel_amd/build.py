@@ -3,6 +3,7 @@
 Produces, in-tree:
   grouped_gemm_gpu_kernel_amd/lib/libgrouped_gemm_amd.so   the library (C-ABI + C++ API)
   grouped_gemm_gpu_kernel_amd/_build/bin/test_correctness   C++ drop-in test driver
+  grouped_gemm_gpu_kernel_amd/_build/bin/benchmark_grouped_gemm   benchmark harness (reference CLI)
   oracle/liboracle.so                                       CPU oracle (test infrastructure)
 
 Steps: hipcc compiles the kernels for gfx950 with the compiler's resource
@@ -143,6 +144,18 @@ def build_cpp_tests() -> Path:
     return exe
 
 
+def build_bench_driver() -> Path:
+    """The benchmark harness (bench/benchmark_grouped_gemm.cpp): the reference
+    benchmark's command line, table and fixed-output cache on this library."""
+    bin_dir = BUILD / "bin"
+    bin_dir.mkdir(parents=True, exist_ok=True)
+    exe = bin_dir / "benchmark_grouped_gemm"
+    src = PKG / "bench" / "benchmark_grouped_gemm.cpp"
+    _run([*CXX_FLAGS, str(src), "-o", str(exe), f"-L{LIB_DIR}", "-lgrouped_gemm_amd",
+          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{LIB_DIR}", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    return exe
+
+
 def build_oracle() -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     return ROOT / "oracle" / "liboracle.so"
@@ -154,6 +167,7 @@ def main(argv: list[str]) -> int:
         build_oracle()
     if "--no-tests" not in argv:
         build_cpp_tests()
+    build_bench_driver()
     print(f"built {LIB_DIR / LIB_NAME}")
     return 0
 

@@ -106,12 +106,18 @@ template <int V, int PATH> struct KernelShape;
 #ifndef GG_WORK_TN
 #define GG_WORK_TN 2
 #endif
+#ifndef GG_WAVE_N
+#define GG_WAVE_N 64
+#endif
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
-  static constexpr int TM = GG_WORK_TM;  // reference tiles per work tile, along M
-  static constexpr int TN = GG_WORK_TN;  // and along N
+  // GG_WORK_TM / GG_WORK_TN / GG_WAVE_N retune the 128x64x32 variant only.
+  static constexpr bool kTuned = V == GGK_VARIANT_128x64x32;
+  static constexpr int TM = kTuned ? GG_WORK_TM : 2;  // reference tiles per work tile, along M
+  static constexpr int TN = kTuned ? GG_WORK_TN : 2;  // and along N
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
-  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, (BM / 64) * (BN / 64) * kWave>;
+  static constexpr int WAVE_N = kTuned && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave
+  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, (BM / 64) * (BN / WAVE_N) * kWave>;
 };
 template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr int TM = 1;

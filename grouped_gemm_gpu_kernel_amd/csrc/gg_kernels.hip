@@ -111,10 +111,13 @@ __device__ __forceinline__ int work_tiles_n(const gg_device_problem_desc& p) {
   return (p.tiles_n + TN - 1) / TN;
 }
 
-// At most 256 VGPRs + AGPRs per lane: two waves per SIMD (a 512-thread
-// workgroup, or two 256-thread ones).
+// At least GG_WAVES_PER_EU waves per SIMD: 2 allows 256 VGPRs + AGPRs per lane
+// (a 512-thread workgroup, or two 256-thread ones).
+#ifndef GG_WAVES_PER_EU
+#define GG_WAVES_PER_EU 2
+#endif
 #define GG_KERNEL_ATTRS(V, PATH) \
-  __launch_bounds__((KernelShape<V, PATH>::G::THREADS)) __attribute__((amdgpu_waves_per_eu(2)))
+  __launch_bounds__((KernelShape<V, PATH>::G::THREADS)) __attribute__((amdgpu_waves_per_eu(GG_WAVES_PER_EU)))
 
 template <int V, int PATH, bool TRACED, bool WIDE>
 __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {

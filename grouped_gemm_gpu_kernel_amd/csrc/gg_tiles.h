@@ -73,9 +73,9 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
 template <class G>
 struct MfmaTile {
   static constexpr int WM = 64;
-  static constexpr int WN = 64;
   static constexpr int WAVES_M = G::BM / WM;
-  static constexpr int WAVES_N = G::BN / WN;
+  static constexpr int WAVES_N = G::THREADS / kWave / WAVES_M;
+  static constexpr int WN = G::BN / WAVES_N;
   static constexpr int FM = WM / 32;
   static constexpr int FN = WN / 32;
   static_assert(WAVES_M * WAVES_N * kWave == G::THREADS, "one wave per block of D");

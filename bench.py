@@ -36,6 +36,8 @@ def parse_args():
     ap.add_argument("--modes", default="0,1,2,3", help="sort modes to time")
     ap.add_argument("--no-baseline", action="store_true", help="skip the per-problem-launch baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-torch-op", action="store_true", help="skip the torch binding timings")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the hipBLASLt comparison rows")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--fma", action="store_true", help="FMA tile path instead of MFMA")
     ap.add_argument("--table", action="store_true", help="also print the reference-style results table")
@@ -61,10 +63,10 @@ def calibrate_copy(torch, mib: int) -> int:
 
 def time_runs(torch, fn, steps: int, warmup: int) -> float:
     """Mean ms per call over `steps` calls after `warmup`, HIP events on the current stream (the
-    stream fn launches on)."""
+    stream fn launches on).  fn returns a hipError_t (non-zero raises) or raises itself."""
     for _ in range(warmup):
         st = fn()
-        if st != 0:
+        if isinstance(st, int) and st != 0:
             raise RuntimeError(f"hipError_t {st}")
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -72,7 +74,7 @@ def time_runs(torch, fn, steps: int, warmup: int) -> float:
     start.record()
     for _ in range(steps):
         st = fn()
-        if st != 0:
+        if isinstance(st, int) and st != 0:
             raise RuntimeError(f"hipError_t {st}")
     stop.record()
     stop.synchronize()
@@ -94,6 +96,42 @@ def measured_tail_idle(torch, ex) -> float:
     if t1 <= t0:
         return 0.0
     return float(((t1 - c[:, 1]).sum()) / (grid * (t1 - t0)))
+
+
+def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int) -> dict:
+    """The same workload through the torch binding: GroupedGemmPlan.run() (device time, events on
+    the launch stream) and one-shot run_grouped_gemm (host wall time per call: prepare, upload,
+    launch, wait, release)."""
+    from grouped_gemm_gpu_kernel_amd import torch_ops
+
+    a, b, c, d, alpha, beta = dw.tensors()
+    plan = torch_ops.GroupedGemmPlan(a, b, c if dw.has_c else None, d, alpha, beta, sort_mode=mode, config=cfg)
+    plan_ms = time_runs(torch, lambda: plan.run(stream), steps, warmup)
+    plan.close()
+    calls = 5
+    torch_ops.run_grouped_gemm(a, b, c if dw.has_c else None, alpha, beta, sort_mode=mode, config=cfg, out=d)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        torch_ops.run_grouped_gemm(a, b, c if dw.has_c else None, alpha, beta, sort_mode=mode, config=cfg, out=d)
+    one_shot_ms = (time.perf_counter() - t0) * 1e3 / calls
+    out = {"sort_mode": mode.name, "plan_run_ms": round(plan_ms, 4), "one_shot_wall_ms": round(one_shot_ms, 3)}
+    print(f"# torch binding {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def vendor_baseline(spec, config_name: str, sort_mode: int, steps: int, warmup: int):
+    """The same problem set through hipBLASLt, in a child process (see grouped_gemm_gpu_kernel_amd/
+    vendor.py): its grouped GEMM (every heuristic candidate timed, the fastest kept) and one vendor
+    GEMM per problem, each checked element by element against this library's D on the same
+    operands.  Rows read {"error": ...} where the vendor library has no algorithm."""
+    from grouped_gemm_gpu_kernel_amd import vendor
+
+    try:
+        res = vendor.run(spec, steps=steps, warmup=warmup, config=config_name, sort_mode=sort_mode)
+    except Exception as exc:  # reported in the JSON line, not fatal to the bench
+        res = {"error": str(exc)}
+    print(f"# vendor {res}", file=sys.stderr, flush=True)
+    return res
 
 
 def cpu_baseline(dw, spec, seconds: float):
@@ -259,6 +297,11 @@ def main() -> int:
                     "launches": api.count_non_empty_problems(probs, cfg)}
         print(f"# {baseline}", file=sys.stderr, flush=True)
 
+    best_mode = next(m for m in modes if api.sort_mode_name(m) == best[0]["mode"])
+    vendor_rows = None if (args.no_vendor or args.fma) else vendor_baseline(spec, config_name, int(best_mode),
+                                                                            args.steps, args.warmup)
+    torch_op = None if args.no_torch_op else torch_binding(torch, dw, cfg, best_mode, stream, args.steps,
+                                                          args.warmup)
     cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds)
 
     row, ms = best
@@ -303,6 +346,8 @@ def main() -> int:
         "speedup_vs_per_problem_baseline": round(baseline["kernel_ms"] / ms, 2) if baseline else None,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "torch_op": torch_op,
+        "vendor_hipblaslt": vendor_rows,
     }
     if args.table:
         print(f"{'mode':24}{'prep_ms':>10}{'kernel_ms':>11}{'tflops':>10}{'tiles':>8}{'grid':>7}{'launches':>10}"

@@ -4,6 +4,7 @@ Produces, in-tree:
   grouped_gemm_gpu_kernel_amd/lib/libgrouped_gemm_amd.so   the library (C-ABI + C++ API)
   grouped_gemm_gpu_kernel_amd/_build/bin/test_correctness   C++ drop-in test driver
   grouped_gemm_gpu_kernel_amd/_build/bin/benchmark_grouped_gemm   benchmark harness (reference CLI)
+  grouped_gemm_gpu_kernel_amd/_build/bin/vendor_hipblaslt   hipBLASLt comparison program (bench only)
   oracle/liboracle.so                                       CPU oracle (test infrastructure)
 
 Steps: hipcc compiles the kernels for gfx950 with the compiler's resource
@@ -156,6 +157,18 @@ def build_bench_driver() -> Path:
     return exe
 
 
+def build_vendor_baseline() -> Path:
+    """The hipBLASLt comparison program (bench/vendor_hipblaslt.cpp), run by
+    bench.py and the tests as a child process; the library does not link it."""
+    bin_dir = BUILD / "bin"
+    bin_dir.mkdir(parents=True, exist_ok=True)
+    exe = bin_dir / "vendor_hipblaslt"
+    src = PKG / "bench" / "vendor_hipblaslt.cpp"
+    _run([*CXX_FLAGS, str(src), "-o", str(exe), f"-L{LIB_DIR}", "-lgrouped_gemm_amd", f"-L{ROCM / 'lib'}",
+          "-lhipblaslt", "-lamdhip64", f"-Wl,-rpath,{LIB_DIR}", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    return exe
+
+
 def build_oracle() -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     return ROOT / "oracle" / "liboracle.so"
@@ -168,6 +181,7 @@ def main(argv: list[str]) -> int:
     if "--no-tests" not in argv:
         build_cpp_tests()
     build_bench_driver()
+    build_vendor_baseline()
     print(f"built {LIB_DIR / LIB_NAME}")
     return 0
 

@@ -1,0 +1,186 @@
+"""PyTorch binding: the grouped GEMM on lists of torch tensors.
+
+    d_i = alpha_i * a_i @ b_i + beta_i * c_i      for every i, in one persistent launch
+
+a_i: float16 [m_i, k_i], b_i: float16 [k_i, n_i], c_i: float32 [m_i, n_i] or None, d_i: float32
+[m_i, n_i]; products accumulate in float32 (the contract of the reference's ProblemDesc,
+include/grouped_gemm/grouped_gemm.cuh:18-35).  Rows may be padded (a row stride above the row
+length, e.g. a column slice of a wider tensor); elements inside a row must be contiguous.
+
+Two forms:
+* run_grouped_gemm(a, b, c, alpha, beta, ...) -- one call, the reference's run_grouped_gemm_once
+  (src/grouped_gemm.cu:1279-1291): prepares, uploads, launches on the current stream and waits for
+  it, because the executor's device buffers are released before it returns.  Registered as the
+  custom op torch.ops.grouped_gemm_amd.grouped_gemm.
+* GroupedGemmPlan(a, b, c, d, ...) -- prepare and upload once, then run() any number of times on
+  any stream without host synchronisation, as the reference's GroupedGemmExecutor is used
+  (include/grouped_gemm/grouped_gemm.cuh:94-115).  The plan holds its tensors; refill them in place
+  between runs.
+
+All work runs in the HIP library (lib/libgrouped_gemm_amd.so); there is no CPU fallback.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+from .api import GroupedGemmExecutor, KernelConfig, ProblemDesc, SortMode, prepare_problem_set
+
+Scalars = Union[float, Sequence[float]]
+
+_OP_NAME = "grouped_gemm_amd::grouped_gemm"
+_placeholders: dict = {}
+
+
+def _placeholder(device: torch.device) -> int:
+    """A valid device address for operands with no elements (the library rejects null a/b/d
+    pointers even where nothing is read, src/grouped_gemm.cu:1304-1307)."""
+    key = (device.type, device.index)
+    if key not in _placeholders:
+        _placeholders[key] = torch.zeros(64, dtype=torch.float32, device=device)
+    return _placeholders[key].data_ptr()
+
+
+def _row_stride(t: torch.Tensor) -> int:
+    rows, cols = t.shape
+    if rows <= 1 or t.numel() == 0:  # the stride of an empty or one-row matrix is never used
+        return max(1, cols)
+    return t.stride(0)
+
+
+def _check_matrix(t: torch.Tensor, name: str, dtype: torch.dtype, shape, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    rows, cols = t.shape
+    if t.numel() == 0:
+        return
+    if cols > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name} must have contiguous rows (stride(1) == 1)")
+    if rows > 1 and t.stride(0) < max(1, cols):
+        raise ValueError(f"{name} rows overlap (stride(0) < shape[1])")
+
+
+def _per_problem(values: Scalars, count: int, name: str) -> list:
+    if isinstance(values, (int, float)):
+        return [float(values)] * count
+    values = [float(v) for v in values]
+    if len(values) != count:
+        raise ValueError(f"{name} has {len(values)} entries for {count} problems")
+    return values
+
+
+def _problems(a, b, c, d, alpha, beta):
+    count = len(a)
+    if len(b) != count or len(d) != count or (c is not None and len(c) != count):
+        raise ValueError("a, b, c and d must hold one tensor per problem")
+    if count == 0:
+        return []
+    device = a[0].device
+    if device.type != "cuda":
+        raise ValueError(f"tensors must be on a GPU, got {device}")
+    alpha = _per_problem(alpha, count, "alpha")
+    beta = _per_problem(beta, count, "beta")
+    dummy = _placeholder(device)
+    problems = []
+    for i in range(count):
+        _check_matrix(a[i], f"a[{i}]", torch.float16, None, device)
+        m, k = a[i].shape
+        _check_matrix(b[i], f"b[{i}]", torch.float16, None, device)
+        if b[i].shape[0] != k:
+            raise ValueError(f"b[{i}] has {b[i].shape[0]} rows, a[{i}] has {k} columns")
+        n = b[i].shape[1]
+        _check_matrix(d[i], f"d[{i}]", torch.float32, (m, n), device)
+        ci = None if c is None else c[i]
+        if ci is not None:
+            _check_matrix(ci, f"c[{i}]", torch.float32, (m, n), device)
+        problems.append(ProblemDesc(
+            m=m, n=n, k=k,
+            a=a[i].data_ptr() or dummy, b=b[i].data_ptr() or dummy,
+            c=(ci.data_ptr() or dummy) if ci is not None else None,
+            d=d[i].data_ptr() or dummy,
+            lda=_row_stride(a[i]), ldb=_row_stride(b[i]),
+            ldc=_row_stride(ci) if ci is not None else max(1, n), ldd=_row_stride(d[i]),
+            alpha=alpha[i], beta=beta[i]))
+    return problems
+
+
+class GroupedGemmPlan:
+    """A prepared grouped GEMM over fixed tensors: prepare_problem_set + executor build once,
+    run() per use.  Runs are stream-ordered and must not overlap each other (one scheduler state
+    per plan, as one per executor in the reference)."""
+
+    def __init__(self, a: Sequence[torch.Tensor], b: Sequence[torch.Tensor],
+                 c: Optional[Sequence[Optional[torch.Tensor]]], d: Sequence[torch.Tensor],
+                 alpha: Scalars = 1.0, beta: Scalars = 0.0, *, sort_mode: int = SortMode.kByK,
+                 config: Optional[KernelConfig] = None):
+        self.config = config if config is not None else KernelConfig.named("128x64x32")
+        self.problems = _problems(a, b, c, d, alpha, beta)
+        self._tensors = (list(a), list(b), None if c is None else list(c), list(d))
+        self.prepared = prepare_problem_set(self.problems, self.config, sort_mode)
+        self.executor = GroupedGemmExecutor()
+        self.device = a[0].device if len(a) else None
+        if self.problems:
+            with torch.cuda.device(self.device):
+                _lib.check(self.executor.build(self.prepared, self.config), "GroupedGemmExecutor.build")
+
+    @property
+    def outputs(self) -> list:
+        return self._tensors[3]
+
+    def run(self, stream: Optional[torch.cuda.Stream] = None) -> list:
+        if not self.problems:
+            return self.outputs
+        with torch.cuda.device(self.device):
+            stream = stream if stream is not None else torch.cuda.current_stream(self.device)
+            _lib.check(self.executor.run(stream), "GroupedGemmExecutor.run")
+        return self.outputs
+
+    def close(self) -> None:
+        self.executor.close()
+
+
+def run_grouped_gemm(a: Sequence[torch.Tensor], b: Sequence[torch.Tensor],
+                     c: Optional[Sequence[Optional[torch.Tensor]]] = None, alpha: Scalars = 1.0,
+                     beta: Scalars = 0.0, *, sort_mode: int = SortMode.kByK,
+                     config: Optional[KernelConfig] = None,
+                     out: Optional[Sequence[torch.Tensor]] = None) -> list:
+    """One grouped launch on the current stream; returns d (allocated unless given as out).
+    Waits for the launch before returning (see the module docstring)."""
+    if out is None:
+        if len(a) and len(b) != len(a):
+            raise ValueError("a and b must hold one tensor per problem")
+        out = [torch.empty((ai.shape[0], bi.shape[1] if bi.dim() == 2 else 0), dtype=torch.float32,
+                           device=ai.device) for ai, bi in zip(a, b)]
+    plan = GroupedGemmPlan(a, b, c, out, alpha, beta, sort_mode=sort_mode, config=config)
+    try:
+        plan.run()
+    finally:
+        plan.close()  # synchronises the device, then releases the plan's descriptor buffers
+    return list(out)
+
+
+# ---------------------------------------------------------------- custom op
+
+@torch.library.custom_op(_OP_NAME, mutates_args=())
+def _grouped_gemm_op(a: list[torch.Tensor], b: list[torch.Tensor], c: list[Optional[torch.Tensor]],
+                     alpha: list[float], beta: list[float], sort_mode: int) -> list[torch.Tensor]:
+    """c: one entry per problem (None where C is not read), or an empty list for no C at all."""
+    return run_grouped_gemm(a, b, c if len(c) else None, alpha, beta, sort_mode=sort_mode)
+
+
+@_grouped_gemm_op.register_fake
+def _grouped_gemm_fake(a, b, c, alpha, beta, sort_mode):
+    return [ai.new_empty((ai.shape[0], bi.shape[1]), dtype=torch.float32) for ai, bi in zip(a, b)]
+
+
+grouped_gemm_op = _grouped_gemm_op

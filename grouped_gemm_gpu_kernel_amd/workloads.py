@@ -222,6 +222,26 @@ class DeviceWorkload:
                 alpha=float(spec.alpha[i]), beta=float(spec.beta[i])))
         return out
 
+    def tensors(self):
+        """Per-problem torch views (a fp16 [m, k], b fp16 [k, n], c fp32 [m, n] or None, d fp32
+        [m, n]) of the pools, for the torch binding."""
+        import torch
+
+        spec = self.spec
+        a, b, c, d = [], [], [], []
+        for i in range(spec.count):
+            mi, ni, ki = int(spec.m[i]), int(spec.n[i]), int(spec.k[i])
+
+            def view(pool, off, rows, cols, dtype):
+                flat = pool[int(off):int(off) + rows * cols]
+                return (flat.view(dtype) if dtype != pool.dtype else flat).view(rows, cols)
+
+            a.append(view(self.a, self.a_off[i], mi, ki, torch.float16))
+            b.append(view(self.b, self.b_off[i], ki, ni, torch.float16))
+            c.append(view(self.c, self.c_off[i], mi, ni, torch.float32) if self.has_c else None)
+            d.append(view(self.d, self.d_off[i], mi, ni, torch.float32))
+        return a, b, c, d, [float(x) for x in spec.alpha], [float(x) for x in spec.beta]
+
     # Host copies of one problem's operands (tests and the CPU baseline).
     def host_a(self, i: int) -> np.ndarray:
         n = _elems(int(self.spec.m[i]), int(self.spec.k[i]))

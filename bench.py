@@ -119,6 +119,36 @@ def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int) -> dict
     return out
 
 
+def moe_device_prepare(torch, dw, spec, cfg, mode, stream, steps: int, warmup: int):
+    """A group whose problems share n and k and read no C (moe64) through the device-side prepare:
+    the expert rows of A stacked into one [T, k] tensor, B as [E, k, n], the int32 counts on the
+    GPU; prepare kernel + grouped launch per run (device time, events on the launch stream), next
+    to the grouped launch alone after the host prepare.  None for other workloads."""
+    import numpy as np
+
+    from grouped_gemm_gpu_kernel_amd import torch_ops
+
+    n, k = int(spec.n[0]), int(spec.k[0])
+    if not ((spec.n == n).all() and (spec.k == k).all()) or dw.has_c:
+        return None
+    rows = np.asarray(spec.m, dtype=np.int64)
+    a_pool = dw.a.view(torch.float16)
+    b_pool = dw.b.view(torch.float16)
+    a = torch.cat([a_pool[int(o):int(o) + int(m) * k].view(int(m), k) for o, m in zip(dw.a_off, rows)])
+    b = torch.stack([b_pool[int(o):int(o) + k * n].view(k, n) for o in dw.b_off])
+    d = torch.empty(int(rows.sum()), n, dtype=torch.float32, device=a.device)
+    counts = torch.from_numpy(rows.astype(np.int32)).cuda()
+    plan = torch_ops.MoeGroupedGemmPlan(a, b, d, None, float(spec.alpha[0]), float(spec.beta[0]), sort_mode=mode,
+                                        config=cfg)
+    ms = time_runs(torch, lambda: plan.run(counts, stream), steps, warmup)
+    status = plan.status()
+    plan.close()
+    del a, b, d
+    out = {"experts": spec.count, "sort_mode": mode.name, "prepare_plus_gemm_ms": round(ms, 4), "status": status}
+    print(f"# moe device prepare {out}", file=sys.stderr, flush=True)
+    return out
+
+
 def vendor_baseline(spec, config_name: str, sort_mode: int, steps: int, warmup: int):
     """The same problem set through hipBLASLt, in a child process (see grouped_gemm_gpu_kernel_amd/
     vendor.py): its grouped GEMM (every heuristic candidate timed, the fastest kept) and one vendor
@@ -298,6 +328,8 @@ def main() -> int:
         print(f"# {baseline}", file=sys.stderr, flush=True)
 
     best_mode = next(m for m in modes if api.sort_mode_name(m) == best[0]["mode"])
+    moe_device = None if args.fma else moe_device_prepare(torch, dw, spec, cfg, best_mode, stream, args.steps,
+                                                          args.warmup)
     vendor_rows = None if (args.no_vendor or args.fma) else vendor_baseline(spec, config_name, int(best_mode),
                                                                             args.steps, args.warmup)
     torch_op = None if args.no_torch_op else torch_binding(torch, dw, cfg, best_mode, stream, args.steps,
@@ -348,6 +380,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "torch_op": torch_op,
         "vendor_hipblaslt": vendor_rows,
+        "moe_device_prepare": moe_device,
     }
     if args.table:
         print(f"{'mode':24}{'prep_ms':>10}{'kernel_ms':>11}{'tflops':>10}{'tiles':>8}{'grid':>7}{'launches':>10}"

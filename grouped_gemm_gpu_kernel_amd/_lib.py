@@ -30,6 +30,11 @@ GGK_ADDR_32 = 0
 GGK_ADDR_64 = 1
 GGK_SCHEDULER_STATE_INTS = 16
 GGK_SCHEDULER_CHUNKS = 8
+GGK_MOE_MAX_EXPERTS = 1024
+GGK_MOE_HEADER_INTS = 16
+GGK_MOE_STATUS = 12
+GGK_MOE_NEGATIVE = 1
+GGK_MOE_CLAMPED = 2
 
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_ll_p = ctypes.POINTER(ctypes.c_longlong)
@@ -90,6 +95,18 @@ class GGKWorkShape(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int) for name in ("tiles_m", "tiles_n", "threads", "rows", "stage_k")]
 
 
+class GGKMoeLayout(ctypes.Structure):
+    """ggk_moe_layout (grouped_gemm_amd_kernels.h)"""
+    _fields_ = [
+        ("experts", ctypes.c_int), ("n", ctypes.c_int), ("k", ctypes.c_int),
+        ("a", ctypes.c_void_p), ("lda", ctypes.c_int),
+        ("b", ctypes.c_void_p), ("ldb", ctypes.c_int), ("stride_b", ctypes.c_longlong),
+        ("c", ctypes.c_void_p), ("ldc", ctypes.c_int),
+        ("d", ctypes.c_void_p), ("ldd", ctypes.c_int),
+        ("alpha", ctypes.c_float), ("beta", ctypes.c_float), ("max_rows", ctypes.c_int),
+    ]
+
+
 _P = ctypes.POINTER
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -117,6 +134,11 @@ SIGNATURES = {
     "gg_run_baseline_per_problem": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _vp]),
     "gg_count_non_empty_problems": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig)]),
     "gg_grid_ctas_for": (_i, [_P(GGKernelConfig), _i]),
+    "gg_moe_create": (_i, [_P(GGKMoeLayout), _P(GGKernelConfig), _i, _P(_vp)]),
+    "gg_moe_run": (_i, [_vp, _vp, _vp]),
+    "gg_moe_grid_ctas": (_i, [_vp]),
+    "gg_moe_device_buffers": (_i, [_vp, _P(_vp), _P(_vp), _P(_vp), _P(_vp)]),
+    "gg_moe_destroy": (None, [_vp]),
     # grouped_gemm_amd_kernels.h
     "ggk_alloc": (_i, [_P(_vp), ctypes.c_size_t]),
     "ggk_free": (_i, [_vp]),
@@ -131,6 +153,8 @@ SIGNATURES = {
     "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
     "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp, _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
+    "ggk_moe_prepare": (_i, [_i, _i, _P(GGKMoeLayout), _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "ggk_launch_grouped_device": (_i, [_i, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _vp]),
     "ggk_kernel_resources_get": (_i, [_i, _i, _i, _P(GGKKernelResources)]),
     "ggk_occupancy": (_i, [_i, _i, c_int_p]),
     "ggk_fill_uniform_f16": (_i, [_vp, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,

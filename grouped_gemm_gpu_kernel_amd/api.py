@@ -14,7 +14,7 @@ from enum import IntEnum
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import GGKernelConfig, GGOccupancyInfo, GGProblemDesc
+from ._lib import GGKernelConfig, GGKMoeLayout, GGOccupancyInfo, GGProblemDesc
 
 
 class SortMode(IntEnum):
@@ -224,6 +224,69 @@ class GroupedGemmExecutor:
 
     def using_tensor_cores(self) -> bool:
         return bool(_lib.lib().gg_executor_using_tensor_cores(self._handle))
+
+
+@dataclass
+class MoeLayout:
+    """A mixture-of-experts group (no reference counterpart, see ggk_moe_prepare): expert e
+    multiplies rows [r_e, r_e + count_e) of A (fp16, rows x k, lda) by B + e * stride_b (fp16,
+    k x n, ldb) into the same rows of D (fp32, ldd), adding beta * C (fp32, ldc) when c is set."""
+    experts: int
+    n: int
+    k: int
+    a: int
+    lda: int
+    b: int
+    ldb: int
+    stride_b: int
+    c: Optional[int]
+    ldc: int
+    d: int
+    ldd: int
+    alpha: float = 1.0
+    beta: float = 0.0
+    max_rows: int = 0
+
+    def to_c(self) -> GGKMoeLayout:
+        return GGKMoeLayout(self.experts, self.n, self.k, self.a or None, self.lda, self.b or None, self.ldb,
+                            self.stride_b, self.c or None, self.ldc, self.d or None, self.ldd, self.alpha,
+                            self.beta, self.max_rows)
+
+
+class MoeGroupedGemm:
+    """MoeGroupedGemm (include/grouped_gemm/grouped_gemm.h): the problem set is prepared on the
+    device from device-side token counts; run() does not synchronise or allocate."""
+
+    def __init__(self, layout: MoeLayout, config: KernelConfig, sort_mode: int = 2):
+        self._handle = ctypes.c_void_p()
+        self.layout = layout
+        st = _lib.lib().gg_moe_create(ctypes.byref(layout.to_c()), ctypes.byref(config.to_c()), int(sort_mode),
+                                      ctypes.byref(self._handle))
+        _lib.check(st, "gg_moe_create")
+
+    def run(self, counts_ptr: int, stream=None) -> int:
+        return _lib.lib().gg_moe_run(self._handle, counts_ptr or None, _stream_handle(stream))
+
+    def grid_ctas(self) -> int:
+        return _lib.lib().gg_moe_grid_ctas(self._handle)
+
+    def device_buffers(self) -> tuple:
+        """(problems, offsets, sorted_to_original, header) device addresses."""
+        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        _lib.check(_lib.lib().gg_moe_device_buffers(self._handle, *[ctypes.byref(p) for p in ptrs]),
+                   "gg_moe_device_buffers")
+        return tuple(p.value or 0 for p in ptrs)
+
+    def close(self) -> None:
+        if self._handle:
+            _lib.lib().gg_moe_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def run_grouped_gemm_once(problems: Sequence[ProblemDesc], sort_mode: int, config: KernelConfig,

@@ -99,21 +99,27 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), c
     build_dir.mkdir(parents=True, exist_ok=True)
     out.parent.mkdir(parents=True, exist_ok=True)
     kernels_o = build_dir / "gg_kernels.o"
+    moe_o = build_dir / "gg_moe.o"
     extra = [f"-D{d}" for d in defines]
 
     def compile_kernels() -> str:
         return _run([HIPCC, *HIP_FLAGS, *extra, "-Rpass-analysis=kernel-resource-usage", "-c",
                      str(CSRC / "gg_kernels.hip"), "-o", str(kernels_o)], capture_stderr=True)
 
+    def compile_moe() -> None:
+        _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / "gg_moe.hip"), "-o", str(moe_o)])
+
     def compile_host(name: str) -> Path:
         obj = build_dir / (Path(name).stem + ".o")
         _run([*CXX_FLAGS, f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)])
         return obj
 
-    with ThreadPoolExecutor(max_workers=3) as pool:
+    with ThreadPoolExecutor(max_workers=4) as pool:
         fut_k = pool.submit(compile_kernels)
+        fut_moe = pool.submit(compile_moe)
         host_objs = list(pool.map(compile_host, ["grouped_gemm.cpp", "c_api.cpp"]))
         report = fut_k.result()
+        fut_moe.result()
 
     rows = parse_resource_report(report)
     if len(rows) != 12:
@@ -124,7 +130,7 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), c
     _run([*CXX_FLAGS, f"-I{build_dir}", "-c", str(CSRC / "gg_resources.cpp"), "-o", str(res_o)])
 
     tmp = out.parent / (out.name + ".tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(kernels_o),
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(kernels_o), str(moe_o),
           *map(str, host_objs), str(res_o)])
     os.replace(tmp, out)
     return out

@@ -24,6 +24,10 @@ struct gg_executor {
   gg::GroupedGemmExecutor executor;
 };
 
+struct gg_moe {
+  gg::MoeGroupedGemm moe;
+};
+
 namespace {
 
 gg::ProblemDesc to_cpp(const gg_problem_desc& p) {
@@ -241,5 +245,55 @@ int gg_grid_ctas_for(const gg_kernel_config* config, int total_tiles) {
   if (status != hipSuccess) return -static_cast<int>(status);
   return gg::grid_ctas_for(total_tiles, cfg, o);
 }
+
+int gg_moe_create(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode, gg_moe** out) {
+  if (out == nullptr) return hipErrorInvalidValue;
+  *out = nullptr;
+  if (layout == nullptr || config == nullptr) return hipErrorInvalidValue;
+  gg_moe* m = new (std::nothrow) gg_moe;
+  if (m == nullptr) return hipErrorOutOfMemory;
+  gg::MoeLayout L;
+  L.experts = layout->experts;
+  L.n = layout->n;
+  L.k = layout->k;
+  L.a = static_cast<const __half*>(layout->a);
+  L.lda = layout->lda;
+  L.b = static_cast<const __half*>(layout->b);
+  L.ldb = layout->ldb;
+  L.stride_b = layout->stride_b;
+  L.c = layout->c;
+  L.ldc = layout->ldc;
+  L.d = layout->d;
+  L.ldd = layout->ldd;
+  L.alpha = layout->alpha;
+  L.beta = layout->beta;
+  L.max_rows = layout->max_rows;
+  const hipError_t status = m->moe.build(L, to_cpp(*config), static_cast<gg::SortMode>(sort_mode));
+  if (status != hipSuccess) {
+    delete m;
+    return status;
+  }
+  *out = m;
+  return hipSuccess;
+}
+
+int gg_moe_run(const gg_moe* moe, const int* d_counts, hipStream_t stream) {
+  if (moe == nullptr) return hipErrorInvalidDevicePointer;
+  return moe->moe.run(d_counts, stream);
+}
+
+int gg_moe_grid_ctas(const gg_moe* moe) { return moe != nullptr ? moe->moe.grid_ctas() : 0; }
+
+int gg_moe_device_buffers(const gg_moe* moe, const gg_device_problem_desc** problems, const int** offsets,
+                          const int** sorted_to_original, const int** header) {
+  if (moe == nullptr) return hipErrorInvalidDevicePointer;
+  if (problems != nullptr) *problems = moe->moe.device_problems();
+  if (offsets != nullptr) *offsets = moe->moe.device_offsets();
+  if (sorted_to_original != nullptr) *sorted_to_original = moe->moe.device_sorted_to_original();
+  if (header != nullptr) *header = moe->moe.device_header();
+  return hipSuccess;
+}
+
+void gg_moe_destroy(gg_moe* moe) { delete moe; }
 
 }  // extern "C"

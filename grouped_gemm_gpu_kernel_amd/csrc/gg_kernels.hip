@@ -57,6 +57,10 @@ struct GroupedArgs {
   int* tile_map;       // traced launches only
   long long* wg_clock; // traced launches only
   int bounds[kChunks + 1];  // chunk c owns work-tile indices [bounds[c], bounds[c + 1])
+  // When set, the total and the bounds are read from this device header
+  // (written by a device-side prepare in stream order) instead of the two
+  // fields above: [1] work tiles, [2, 2 + kChunks] bounds.
+  const int* header;
 };
 
 // Claims the next work-tile index for the calling workgroup (one thread calls it).
@@ -66,14 +70,31 @@ struct GroupedArgs {
 // re-reads.  When a chunk runs dry the workgroup moves on to the next one
 // (stealing); `visit` counts the chunks it has left behind.  Returns total
 // when every chunk is exhausted.
-__device__ __forceinline__ int claim_tile(const GroupedArgs& args, int home, int& visit) {
+__device__ __forceinline__ int claim_tile(const GroupedArgs& args, const int* bounds, int total, int home,
+                                          int& visit) {
   while (visit < kChunks) {
     const int c = (home + visit) % kChunks;
-    const int t = args.bounds[c] + atomicAdd(args.state + c, 1);
-    if (t < args.bounds[c + 1]) return t;
+    const int t = bounds[c] + atomicAdd(args.state + c, 1);
+    if (t < bounds[c + 1]) return t;
     ++visit;
   }
-  return args.total;
+  return total;
+}
+
+// The schedule of one launch in LDS: s[0, kChunks] the chunk bounds, s[kChunks + 1]
+// the work-tile total, from the arguments or from the device header.
+__device__ __forceinline__ void load_schedule(const GroupedArgs& args, int* s) {
+  const int tid = threadIdx.x;
+  if (args.header != nullptr) {
+    if (tid <= kChunks) s[tid] = args.header[2 + tid];
+    if (tid == kChunks + 1) s[tid] = args.header[1];
+  } else {
+#pragma unroll
+    for (int c = 0; c <= kChunks; ++c) {
+      if (tid == c) s[c] = args.bounds[c];
+    }
+    if (tid == kChunks + 1) s[tid] = args.total;
+  }
 }
 
 // Index of the problem that owns index t: the number of problems p with
@@ -126,6 +147,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
   using Tile = typename TileFor<PATH, G>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
   __shared__ int s_claim;
+  __shared__ int s_schedule[kChunks + 2];
 
   const int tid = threadIdx.x;
   long long clock_start = 0;
@@ -138,12 +160,15 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
   const int home = blockIdx.x % kChunks;
   int visit = 0;  // meaningful in thread 0 only
   int next = 0;
-  if (tid == 0) s_claim = claim_tile(args, home, visit);
+  load_schedule(args, s_schedule);
+  __syncthreads();
+  const int total = __builtin_amdgcn_readfirstlane(s_schedule[kChunks + 1]);
+  if (tid == 0) s_claim = claim_tile(args, s_schedule, total, home, visit);
   __syncthreads();
   int t = __builtin_amdgcn_readfirstlane(s_claim);
-  while (t < args.total) {
+  while (t < total) {
     // Claim the next index now; its latency hides behind this tile's work.
-    if (tid == 0) next = claim_tile(args, home, visit);
+    if (tid == 0) next = claim_tile(args, s_schedule, total, home, visit);
 
     const int prob = find_problem(args.work_offsets, args.count, t);
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
@@ -408,7 +433,7 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
   if (traced && d_tile_map != nullptr && d_tile_offsets == nullptr) return hipErrorInvalidDevicePointer;
   if (!bounds_valid(chunk_bounds, total_work)) return hipErrorInvalidValue;
   GroupedArgs args{d_problems, d_tile_offsets, d_work_offsets, problem_count, total_work, d_state,
-                   traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}};
+                   traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}, nullptr};
   fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];
@@ -450,6 +475,24 @@ hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_de
                               const int* chunk_bounds, int grid, hipStream_t stream) {
   return launch_grouped(variant, path, addressing, false, d_problems, nullptr, d_work_offsets, problem_count, total_work,
                         d_state, chunk_bounds, grid, nullptr, nullptr, stream);
+}
+
+hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
+                                     const int* d_work_offsets, int problem_count, const int* d_header,
+                                     int* d_state, int grid, hipStream_t stream) {
+  if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 ||
+      (addressing != GGK_ADDR_32 && addressing != GGK_ADDR_64)) {
+    return hipErrorInvalidValue;
+  }
+  if (problem_count == 0) return hipSuccess;
+  if (d_problems == nullptr || d_work_offsets == nullptr || d_state == nullptr || d_header == nullptr) {
+    return hipErrorInvalidDevicePointer;
+  }
+  GroupedArgs args{d_problems, nullptr, d_work_offsets, problem_count, 0, d_state, nullptr, nullptr, {}, d_header};
+  void* params[] = {&args};
+  const KernelSet& k = kKernels[variant][path];
+  return hipLaunchKernel(reinterpret_cast<const void*>(k.grouped[addressing]), dim3(grid), dim3(k.threads), params,
+                         0, stream);
 }
 
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,

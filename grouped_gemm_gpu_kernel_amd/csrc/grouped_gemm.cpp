@@ -491,4 +491,145 @@ int count_non_empty_problems(const std::vector<ProblemDesc>& problems, const Ker
   return count;
 }
 
+// ---------------------------------------------------------------------------
+// MoeGroupedGemm: device-side prepare + grouped launch (no reference counterpart).
+
+struct MoeGroupedGemm::Impl {
+  ggk_moe_layout layout{};
+  int variant = -1;
+  int path = GGK_PATH_FMA;
+  int addressing = GGK_ADDR_32;
+  int sort_mode = 0;
+  int grid_ctas = 0;
+  DeviceProblemDesc* d_problems = nullptr;
+  int* d_ints = nullptr;  // offsets [2 * (E + 1)] | permutation [E] | header | scheduler state
+  int* d_state = nullptr;
+
+  int* offsets() const { return d_ints; }
+  int* perm() const { return d_ints + 2 * (layout.experts + 1); }
+  int* header() const { return perm() + layout.experts; }
+};
+
+MoeGroupedGemm::MoeGroupedGemm() : impl_(new Impl()) {}
+
+MoeGroupedGemm::~MoeGroupedGemm() {
+  if (impl_ != nullptr) {
+    release(impl_->d_problems, impl_->d_ints, impl_->d_state);
+    delete impl_;
+    impl_ = nullptr;
+  }
+}
+
+MoeGroupedGemm::MoeGroupedGemm(MoeGroupedGemm&& other) noexcept : impl_(other.impl_) { other.impl_ = nullptr; }
+
+MoeGroupedGemm& MoeGroupedGemm::operator=(MoeGroupedGemm&& other) noexcept {
+  if (this != &other) {
+    if (impl_ != nullptr) {
+      release(impl_->d_problems, impl_->d_ints, impl_->d_state);
+      delete impl_;
+    }
+    impl_ = other.impl_;
+    other.impl_ = nullptr;
+  }
+  return *this;
+}
+
+hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode) {
+  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  RuntimeMode mode;
+  hipError_t status = resolve_runtime_mode(config, &mode);
+  if (status != hipSuccess) return status;
+  const int e = layout.experts;
+  const int sm = static_cast<int>(sort_mode);
+  if (e < 1 || e > GGK_MOE_MAX_EXPERTS || sm < 0 || sm > 3) return hipErrorInvalidValue;
+  if (layout.a == nullptr || layout.b == nullptr || layout.d == nullptr) return hipErrorInvalidDevicePointer;
+
+  ggk_moe_layout L{};
+  L.experts = e;
+  L.n = layout.n;
+  L.k = layout.k;
+  L.a = layout.a;
+  L.lda = layout.lda;
+  L.b = layout.b;
+  L.ldb = layout.ldb;
+  L.stride_b = layout.stride_b;
+  L.c = layout.c;
+  L.ldc = layout.ldc;
+  L.d = layout.d;
+  L.ldd = layout.ldd;
+  L.alpha = layout.alpha;
+  L.beta = layout.beta;
+  L.max_rows = layout.max_rows;
+
+  // The addressing form from the strides alone (they bound every in-problem
+  // offset, whatever the counts turn out to be).
+  DeviceProblemDesc probe{};
+  probe.m = std::max(1, L.max_rows);
+  probe.n = std::max(1, L.n);
+  probe.k = L.k;
+  probe.a = L.a;
+  probe.b = L.b;
+  probe.c = L.c;
+  probe.d = L.d;
+  probe.lda = L.lda;
+  probe.ldb = L.ldb;
+  probe.ldc = L.ldc;
+  probe.ldd = L.ldd;
+  probe.alpha = L.alpha;
+  probe.beta = L.beta;
+  probe.tiles_m = 1;
+  probe.tiles_n = 1;
+  const int wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
+  if (wide < 0) return hipErrorInvalidValue;
+
+  release(impl_->d_problems, impl_->d_ints, impl_->d_state);
+  const size_t ints = 2 * static_cast<size_t>(e + 1) + e + GGK_MOE_HEADER_INTS;
+  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems), e * sizeof(DeviceProblemDesc));
+  if (status != hipSuccess) return status;
+  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_ints), ints * sizeof(int));
+  if (status != hipSuccess) return status;
+  status = ggk_zero(impl_->d_ints, ints * sizeof(int));
+  if (status != hipSuccess) return status;
+  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_state), GGK_SCHEDULER_STATE_INTS * sizeof(int));
+  if (status != hipSuccess) return status;
+  status = ggk_zero(impl_->d_state, GGK_SCHEDULER_STATE_INTS * sizeof(int));
+  if (status != hipSuccess) return status;
+
+  OccupancyInfo occupancy{};
+  status = fill_occupancy(config, mode, &occupancy);
+  if (status != hipSuccess) return status;
+  impl_->layout = L;
+  impl_->variant = mode.variant;
+  impl_->path = mode.path;
+  impl_->addressing = wide == 1 ? GGK_ADDR_64 : GGK_ADDR_32;
+  impl_->sort_mode = sm;
+  // The total is known only on the device: one workgroup per resident slot
+  // (or the requested persistent size); idle ones retire at once.
+  impl_->grid_ctas = config.persistent_ctas > 0
+                         ? config.persistent_ctas
+                         : std::max(1, occupancy.sm_count * std::max(1, occupancy.active_blocks_per_sm));
+  return hipSuccess;
+}
+
+hipError_t MoeGroupedGemm::run(const int* d_counts, hipStream_t stream) const {
+  if (impl_ == nullptr || impl_->d_problems == nullptr) return hipErrorInvalidDevicePointer;
+  if (d_counts == nullptr) return hipErrorInvalidDevicePointer;
+  hipError_t status = ggk_moe_prepare(impl_->variant, impl_->path, &impl_->layout, d_counts, impl_->sort_mode,
+                                      impl_->d_problems, impl_->offsets(), impl_->perm(), impl_->header(), stream);
+  if (status != hipSuccess) return status;
+  return ggk_launch_grouped_device(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
+                                   impl_->offsets() + impl_->layout.experts + 1, impl_->layout.experts,
+                                   impl_->header(), impl_->d_state, impl_->grid_ctas, stream);
+}
+
+int MoeGroupedGemm::grid_ctas() const { return impl_ != nullptr ? impl_->grid_ctas : 0; }
+const DeviceProblemDesc* MoeGroupedGemm::device_problems() const {
+  return impl_ != nullptr ? impl_->d_problems : nullptr;
+}
+const int* MoeGroupedGemm::device_offsets() const { return impl_ != nullptr && impl_->d_ints ? impl_->offsets() : nullptr; }
+const int* MoeGroupedGemm::device_sorted_to_original() const {
+  return impl_ != nullptr && impl_->d_ints ? impl_->perm() : nullptr;
+}
+const int* MoeGroupedGemm::device_header() const { return impl_ != nullptr && impl_->d_ints ? impl_->header() : nullptr; }
+
 }  // namespace grouped_gemm

@@ -169,6 +169,84 @@ def run_grouped_gemm(a: Sequence[torch.Tensor], b: Sequence[torch.Tensor],
     return list(out)
 
 
+# ---------------------------------------------------------------- mixture of experts
+
+class MoeGroupedGemmPlan:
+    """The grouped GEMM of a mixture-of-experts layer with device-side token counts:
+
+        d[rows of e] = alpha * a[rows of e] @ b[e] + beta * c[rows of e]     for every expert e
+
+    a: float16 [T, K], the tokens grouped by expert (expert e owns rows [r_e, r_e + counts[e]),
+    r_e = sum of the counts before e); b: float16 [E, K, N]; d (and c): float32 [T, N].  The
+    problem set is prepared on the GPU from the int32 counts tensor at every run() (see
+    ggk_moe_prepare): no host synchronisation, no allocation, so runs can be captured in a CUDA/HIP
+    graph and replayed with new counts.  Rows past T are never touched: counts that add up to more
+    are clamped (status() reports it)."""
+
+    def __init__(self, a: torch.Tensor, b: torch.Tensor, d: torch.Tensor, c: Optional[torch.Tensor] = None,
+                 alpha: float = 1.0, beta: float = 0.0, *, sort_mode: int = SortMode.kByTiles,
+                 config: Optional[KernelConfig] = None):
+        from .api import MoeGroupedGemm, MoeLayout
+
+        if a.device.type != "cuda":
+            raise ValueError(f"tensors must be on a GPU, got {a.device}")
+        if b.dim() != 3:
+            raise ValueError(f"b must be [experts, K, N], got shape {tuple(b.shape)}")
+        experts, k, n = b.shape
+        _check_matrix(a, "a", torch.float16, None, a.device)
+        if a.shape[1] != k:
+            raise ValueError(f"a has {a.shape[1]} columns, b has K = {k}")
+        rows = a.shape[0]
+        _check_matrix(d, "d", torch.float32, (rows, n), a.device)
+        if c is not None:
+            _check_matrix(c, "c", torch.float32, (rows, n), a.device)
+        if b.dtype != torch.float16 or b.device != a.device:
+            raise TypeError("b must be float16 on the same device as a")
+        if n > 1 and b.stride(2) != 1:
+            raise ValueError("b[e] must have contiguous rows")
+        if b.numel() and experts > 1 and b.stride(0) < 1:
+            raise ValueError("b experts overlap")
+        self.device = a.device
+        self.experts = experts
+        self.config = config if config is not None else KernelConfig.named("128x64x32")
+        dummy = _placeholder(a.device)
+        layout = MoeLayout(
+            experts=experts, n=n, k=k,
+            a=a.data_ptr() or dummy, lda=_row_stride(a),
+            b=b.data_ptr() or dummy, ldb=b.stride(1) if k > 1 else max(1, n), stride_b=b.stride(0) if experts > 1 else 0,
+            c=(c.data_ptr() or dummy) if c is not None else None, ldc=_row_stride(c) if c is not None else max(1, n),
+            d=d.data_ptr() or dummy, ldd=_row_stride(d), alpha=float(alpha), beta=float(beta), max_rows=rows)
+        self._tensors = (a, b, c, d)
+        with torch.cuda.device(self.device):
+            self.moe = MoeGroupedGemm(layout, self.config, int(sort_mode))
+
+    @property
+    def output(self) -> torch.Tensor:
+        return self._tensors[3]
+
+    def run(self, counts: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        if counts.dtype != torch.int32 or counts.device != self.device or counts.numel() != self.experts:
+            raise ValueError(f"counts must be int32 [{self.experts}] on {self.device}")
+        if not counts.is_contiguous():
+            raise ValueError("counts must be contiguous")
+        with torch.cuda.device(self.device):
+            stream = stream if stream is not None else torch.cuda.current_stream(self.device)
+            _lib.check(self.moe.run(counts.data_ptr(), stream), "MoeGroupedGemm.run")
+        return self.output
+
+    def status(self) -> int:
+        """Status bits of the last run (GGK_MOE_NEGATIVE, GGK_MOE_CLAMPED); reads device memory,
+        so it waits for the run."""
+        header = self.moe.device_buffers()[3]
+        out = torch.empty(_lib.GGK_MOE_HEADER_INTS, dtype=torch.int32)
+        torch.cuda.synchronize(self.device)
+        _lib.check(_lib.lib().ggk_copy_to_host(out.data_ptr(), header, out.numel() * 4), "copy header")
+        return int(out[_lib.GGK_MOE_STATUS])
+
+    def close(self) -> None:
+        self.moe.close()
+
+
 # ---------------------------------------------------------------- custom op
 
 @torch.library.custom_op(_OP_NAME, mutates_args=())

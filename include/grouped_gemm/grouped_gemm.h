@@ -191,4 +191,60 @@ int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& confi
 // 0 when total_tiles is 0.
 int grid_ctas_for(int total_tiles, const KernelConfig& config, const OccupancyInfo& occupancy);
 
+// ---------------------------------------------------------------------------
+// Additions with no counterpart in the reference: the grouped GEMM of a
+// mixture-of-experts layer, prepared on the device from device-side token
+// counts (see ggk_moe_prepare).  Expert e multiplies rows [r_e, r_e + count_e)
+// of A (rows x k) by B + e * stride_b (k x n) into the same rows of D, adding
+// beta * C when c is set; r_e is the prefix sum of the counts.
+struct MoeLayout {
+  int experts = 0;
+  int n = 0;
+  int k = 0;
+  const __half* a = nullptr;
+  int lda = 0;
+  const __half* b = nullptr;
+  int ldb = 0;
+  int64_t stride_b = 0;  // elements between consecutive experts' B
+  const float* c = nullptr;
+  int ldc = 0;
+  float* d = nullptr;
+  int ldd = 0;
+  float alpha = 1.0f;
+  float beta = 0.0f;
+  int max_rows = 0;  // rows of A, C and D the caller owns; rows past it are dropped
+};
+
+// build() checks the layout and allocates the device-side set once; run()
+// launches the prepare kernel and the grouped kernel on the stream, with no
+// host synchronisation and no allocation, so it can be captured in a HIP
+// graph and replayed with new counts.  Runs must not overlap (one scheduler
+// state per object).
+class MoeGroupedGemm {
+ public:
+  MoeGroupedGemm();
+  ~MoeGroupedGemm();
+  MoeGroupedGemm(const MoeGroupedGemm&) = delete;
+  MoeGroupedGemm& operator=(const MoeGroupedGemm&) = delete;
+  MoeGroupedGemm(MoeGroupedGemm&& other) noexcept;
+  MoeGroupedGemm& operator=(MoeGroupedGemm&& other) noexcept;
+
+  hipError_t build(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode);
+  // d_counts: device int[experts], rows per expert.
+  hipError_t run(const int* d_counts, hipStream_t stream = nullptr) const;
+
+  int grid_ctas() const;
+  // The prepared set as the last run wrote it (device memory, stream order):
+  // experts descriptors, 2 * (experts + 1) offsets (reference tiles, then work
+  // tiles), the permutation, and GGK_MOE_HEADER_INTS header ints.
+  const DeviceProblemDesc* device_problems() const;
+  const int* device_offsets() const;
+  const int* device_sorted_to_original() const;
+  const int* device_header() const;
+
+ private:
+  struct Impl;
+  Impl* impl_;
+};
+
 }  // namespace grouped_gemm

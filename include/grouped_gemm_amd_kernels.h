@@ -174,6 +174,59 @@ hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const int* chunk_bounds, int grid, int* d_tile_map, long long* d_wg_clock,
                                      hipStream_t stream);
 
+/* Device-resident preparation of a mixture-of-experts group (no reference
+ * counterpart: it is the step before the grouped launch in MoE use, done here
+ * without a host round trip).  The E experts share N and K: expert e
+ * multiplies rows [r_e, r_e + count_e) of A (binary16, rows x K, lda) by
+ * B + e * stride_b (binary16, K x N, ldb) into the same rows of D (float,
+ * rows x N, ldd), adding beta * C (float, ldc; NULL for none); r_e is the
+ * exclusive prefix sum of the counts in expert order.  One workgroup reads
+ * d_counts[E] (device memory) and writes, in stream order and with no host
+ * synchronisation: d_problems[E], the descriptors in the order
+ * prepare_problem_set gives for sort_mode (src/grouped_gemm.cu:967-1022);
+ * d_offsets[2 * (E + 1)], the reference tile offsets then the work-tile
+ * offsets; d_sorted_to_original[E]; and d_header[GGK_MOE_HEADER_INTS]:
+ * [0] total tiles, [1] total work tiles, [2, 2 + GGK_SCHEDULER_CHUNKS] the
+ * chunk bounds, [GGK_MOE_STATUS] status bits.  Counts are not trusted: a
+ * negative count is taken as 0 (GGK_MOE_NEGATIVE) and rows at or past
+ * max_rows are dropped (GGK_MOE_CLAMPED), so no launch touches rows outside
+ * [0, max_rows) of A, C and D.  1 <= E <= GGK_MOE_MAX_EXPERTS. */
+#define GGK_MOE_MAX_EXPERTS 1024
+#define GGK_MOE_HEADER_INTS 16
+#define GGK_MOE_STATUS 12
+enum { GGK_MOE_NEGATIVE = 1, GGK_MOE_CLAMPED = 2 };
+
+typedef struct ggk_moe_layout {
+  int experts;
+  int n;
+  int k;
+  const void* a;
+  int lda;
+  const void* b;
+  int ldb;
+  long long stride_b; /* elements between consecutive experts' B */
+  const float* c;
+  int ldc;
+  float* d;
+  int ldd;
+  float alpha;
+  float beta;
+  int max_rows; /* rows of A, C and D the caller owns */
+} ggk_moe_layout;
+
+hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts, int sort_mode,
+                           gg_device_problem_desc* d_problems, int* d_offsets, int* d_sorted_to_original,
+                           int* d_header, hipStream_t stream);
+
+/* The grouped launch of a device-prepared set: the same kernel as
+ * ggk_launch_grouped, which reads the work-tile total and the chunk bounds
+ * from d_header (as ggk_moe_prepare writes it) when it starts.  grid is fixed
+ * by the caller (e.g. every resident workgroup); workgroups that find no work
+ * retire at once. */
+hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
+                                     const int* d_work_offsets, int problem_count, const int* d_header,
+                                     int* d_state, int grid, hipStream_t stream);
+
 /* One problem, one workgroup per work tile, row-major work-tile order
  * (single_problem_gemm_kernel + launch_single_problem_variant,
  * src/grouped_gemm.cu:677-688, 753-769).  *problem is read on the host and

@@ -28,10 +28,13 @@ constexpr int kWave = 64;
 // src/grouped_gemm.cu:47-65) fixes the tile -> problem mapping; a work tile
 // covers a whole number of those tiles.
 //
-// LDS layout of one stage (binary16), double buffered:
-//   A: BM rows of SA = BK + 8 values, row-major as in global memory.  The 8
-//      values of padding put the 16-byte operand reads of 16 consecutive rows
-//      on distinct banks.
+// LDS layout of one stage (binary16), BUFFERS stages:
+//   A: BM rows of BK values, each row's 16-byte pieces stored at piece index
+//      (c ^ a_swizzle(row)).  64 banks x 4 bytes hold 256 bytes, i.e. 256 / (2 BK)
+//      rows; the swizzle gives the rows that share a bank window distinct
+//      piece positions, so the 16-byte operand reads of 16 consecutive rows hit
+//      distinct banks.  Rows are not padded: a 64-lane load straight into LDS
+//      writes 1 KB contiguously.
 //   B: BK rows of BN values, row-major as in global memory, with the 8-byte
 //      chunks of row k stored at chunk index (c ^ b_swizzle(k)).  The
 //      transposing operand read touches 4 consecutive rows x 16 columns per
@@ -39,23 +42,33 @@ constexpr int kWave = 64;
 //      padding.  It flips only chunk-index bits >= 3, so 16-byte pieces
 //      (2 chunks) stay contiguous and every 32-column block stays intact.
 //
-// DEPTH stages are in flight in registers at once: the loads of stage k + DEPTH - 1
-// are issued while stage k is multiplied (a ring of DEPTH register sets).
-template <int BM_, int BN_, int BK_, int DEPTH_, int THREADS_>
+// Register staging: DEPTH stages are in flight in registers at once, the
+// loads of stage k + DEPTH - 1 issued while stage k is multiplied (a ring of
+// DEPTH register sets), written to two LDS buffers.  Loads straight into LDS
+// use BUFFERS LDS buffers, BUFFERS - 1 stages in flight.
+template <int BM_, int BN_, int BK_, int DEPTH_, int THREADS_, int BUFFERS_ = 2, bool A_SWIZZLED_ = false>
 struct Geometry {
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int BK = BK_;
   static constexpr int DEPTH = DEPTH_;
   static constexpr int THREADS = THREADS_;
+  static constexpr int BUFFERS = BUFFERS_;
+  // Swizzled, unpadded A rows (needed by loads straight into LDS), or rows
+  // padded by 8 values (the FMA tile, whose operand reads then need no
+  // per-piece index arithmetic).
+  static constexpr bool A_SWIZZLED = A_SWIZZLED_;
   static_assert(DEPTH >= 2, "at least one stage must be in flight while another is multiplied");
+  static_assert(BUFFERS >= 2, "at least double buffered");
   static_assert(THREADS % kWave == 0, "whole waves");
-  static constexpr int SA = BK + 8;
+  static constexpr int SA = A_SWIZZLED ? BK : BK + 8;
   static constexpr int SB = BN;
+  static constexpr int APR = BK / 8;  // 16-byte pieces per A row
+  static_assert(APR == 4 || APR == 8, "A swizzle is defined for 32- and 64-deep stages");
   static constexpr int A_STAGE = BM * SA;  // halves
   static constexpr int B_STAGE = BK * SB;  // halves
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LDS_HALVES = 2 * STAGE;
+  static constexpr int LDS_HALVES = BUFFERS * STAGE;
   // 16-byte pieces per stage and per thread.
   static constexpr int A_VECS = BM * BK / 8;
   static constexpr int B_VECS = BK * BN / 8;
@@ -79,6 +92,14 @@ struct Geometry {
   // Element offset, within a B stage, of the 4-value chunk that holds (k, n)
   // for n a multiple of 4.
   __device__ static __forceinline__ int b_chunk(int k, int n) { return k * SB + 4 * ((n >> 2) ^ b_swizzle(k)); }
+
+  // A: rows that share a 256-byte bank window (row / RPW equal) get distinct
+  // piece positions; RPW = 256 / (2 BK) rows per window.
+  static constexpr int A_RPW = 128 / BK;
+  __device__ static __forceinline__ int a_swizzle(int row) { return A_SWIZZLED ? (row / A_RPW) & (APR - 1) : 0; }
+  // Element offset, within an A stage, of the 16-byte piece c (values 8c ..
+  // 8c + 7 of the stage's k range) of a row.
+  __device__ static __forceinline__ int a_piece(int row, int c) { return row * SA + 8 * (c ^ a_swizzle(row)); }
 };
 
 #ifndef GG_STAGE_K
@@ -117,7 +138,11 @@ template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
   static constexpr int WAVE_N = kTuned && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave
-  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, (BM / 64) * (BN / WAVE_N) * kWave>;
+  static constexpr int THREADS = (BM / 64) * (BN / WAVE_N) * kWave;
+  // Stages load straight into LDS: three buffers (two stages in flight) for the
+  // 512-thread tiles, which have a CU to themselves; two for the 256-thread
+  // tile, so that two of its workgroups share a CU.
+  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, THREADS, THREADS >= 512 ? 3 : 2, true>;
 };
 template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr int TM = 1;
@@ -315,6 +340,7 @@ struct StageLoader<G, false> {
   static constexpr int A_LDS_STEP = (T / APR) * G::SA;
   static constexpr int B_LDS_STEP = (T / BPR) * G::SB;
   static_assert((T / BPR) % 4 == 0, "a thread's B pieces must share their swizzle");
+  static_assert(!G::A_SWIZZLED || (T / APR) % (G::A_RPW * APR) == 0, "a thread's A pieces must share their swizzle");
 
   const gg_device_problem_desc& p;
   __amdgpu_buffer_rsrc_t a_rsrc;  // A from (m0, 0) to the matrix end
@@ -341,7 +367,7 @@ struct StageLoader<G, false> {
     b_off = 2u * ((uint32_t)(tid / BPR) * (uint32_t)p.ldb + (uint32_t)(8 * (tid % BPR)));
     a_step = 2u * (uint32_t)(T / APR) * (uint32_t)p.lda;
     b_step = 2u * (uint32_t)(T / BPR) * (uint32_t)p.ldb;
-    a_lds = (tid / APR) * G::SA + 8 * (tid % APR);
+    a_lds = G::a_piece(tid / APR, tid % APR);  // the thread's pieces share the swizzle (rows 64 apart)
     b_lds = G::b_chunk(tid / BPR, 8 * (tid % BPR));
     last_stage = (p.k - 1) / G::BK;
     a_last = p.k > 0 ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
@@ -432,7 +458,7 @@ struct StageLoader<G, true> {
     for (int i = 0; i < NA; ++i) {
       const int v = t + i * T;
       const EdgePlace e = a_edge(i, kt);
-      *reinterpret_cast<u32x4_t*>(as + (v / APR) * G::SA + 8 * (v % APR)) = finish_piece(r.a[i], e.lead, e.nvalid);
+      *reinterpret_cast<u32x4_t*>(as + G::a_piece(v / APR, v % APR)) = finish_piece(r.a[i], e.lead, e.nvalid);
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -442,6 +468,171 @@ struct StageLoader<G, true> {
     }
   }
 };
+
+// One 16-byte load per lane straight into LDS: lane l's piece, read through
+// the raw buffer resource {base, num_records} at byte offset voff + soff
+// (range-checked per dword like any buffer load), lands at LDS byte address
+// lds + 16 l.  Written as inline assembly on purpose: the compiler's
+// wait-count pass, which cannot tell one LDS stage buffer from another, would
+// otherwise put a wait for every load in flight before each LDS read, which
+// serialises the stage pipeline.  Callers wait for these loads themselves
+// (wait_vmcnt); the compiler's own waits stay correct because loads complete
+// in order.  M0 holds the LDS address; nothing else in these kernels uses M0.
+__device__ __forceinline__ void load_to_lds16(const void* base, uint32_t num_records, uint32_t lds, uint32_t voff,
+                                              uint32_t soff) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const u32x4_t rsrc = {static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b))),
+                        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32))) & 0xffffu,
+                        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(num_records)), 0x00020000u};
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GG_LDS const void*)p));
+}
+
+// Stage loads straight into LDS (buffer_load_dwordx4 ... lds), 32-bit offsets.
+//
+// A load instruction writes its 64 lanes' 16-byte pieces to 1 KB of LDS in
+// lane order, so the LDS layout is fixed by the instruction and the swizzle
+// is applied on the global side: lane l of wave w's instruction i fills LDS
+// slot s = (i * WAVES + w) * 64 + l of the stage's A (or B) part, i.e. row
+// s / PIECES_PER_ROW at piece position s % PIECES_PER_ROW, and therefore
+// fetches the global piece that position holds (position ^ swizzle(row)).
+// A thread's pieces are rows 8 * WAVES (A) or 4 * WAVES (B, 128 columns)
+// apart, which keeps one swizzle per thread, so piece i's global offset is
+// piece 0's plus a wave-uniform step (scalar offset operand).
+//
+// Range checks do what the register path's masking did, except inside the
+// stage that holds k = K - 1: A values at k >= K there are the next row's
+// head, and a final value whose dword straddles the end of a matrix reads as
+// zero.  fix_last_stage repairs the thread's own pieces of that stage in LDS
+// once its loads have landed.
+template <class G>
+struct DmaLoader {
+  static_assert(G::A_SWIZZLED, "a load into LDS writes unpadded rows");
+  static constexpr int T = G::THREADS;
+  static constexpr int WAVES = T / kWave;
+  static constexpr int NA = G::A_PER_THREAD;
+  static constexpr int NB = G::B_PER_THREAD;
+  static constexpr int APR = G::APR;     // A pieces per row
+  static constexpr int BPR = G::BN / 8;  // B pieces per k-row
+  static_assert((kWave * WAVES / APR) % (G::A_RPW * APR) == 0, "a thread's A pieces must share their swizzle");
+  static_assert((kWave * WAVES / BPR) % 4 == 0, "a thread's B pieces must share their swizzle");
+  static constexpr int A_ROWS_STEP = kWave * WAVES / APR;  // rows between a thread's A pieces
+  static constexpr int B_ROWS_STEP = kWave * WAVES / BPR;  // k-rows between a thread's B pieces
+  static constexpr int LOADS = NA + NB;                    // load instructions per stage and wave
+
+  int m, n, k, ldb;
+  const uint16_t* a_tile;  // A at (m0, 0)
+  int64_t a_bytes;         // bytes from a_tile to the end of A
+  const uint16_t* b_tile;  // B at (0, n0)
+  int64_t b_bytes;         // bytes from b_tile to the end of B
+  uint32_t a_off, b_off;   // byte offset of this thread's piece 0 from its origin
+  uint32_t a_step, b_step; // byte distance between a thread's pieces (wave-uniform)
+  int wave;                // wave index (uniform)
+  int a_row, a_col8;       // piece 0: tile row and global piece index within the stage
+  int b_row, b_col8;       // piece 0: k-row within the stage and global piece index
+  int m0, n0;
+  int last_stage;
+  uint32_t a_last, b_last;
+
+  __device__ __forceinline__ DmaLoader(const gg_device_problem_desc& p, int m0_, int n0_)
+      : m(p.m), n(p.n), k(p.k), ldb(p.ldb), m0(m0_), n0(n0_) {
+    const int tid = opaque_tid();
+    const int lane = tid & (kWave - 1);
+    wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint16_t* A = static_cast<const uint16_t*>(p.a);
+    const uint16_t* B = static_cast<const uint16_t*>(p.b);
+    a_tile = A + (int64_t)m0 * p.lda;
+    a_bytes = 2 * ((int64_t)(p.m - 1 - m0) * p.lda + p.k);
+    b_tile = B + n0;
+    b_bytes = 2 * ((int64_t)(p.k - 1) * p.ldb + p.n - n0);
+    const int sa = wave * kWave + lane;  // A slot of piece 0
+    a_row = sa / APR;
+    a_col8 = (sa % APR) ^ G::a_swizzle(a_row);
+    const int sb = wave * kWave + lane;  // B slot of piece 0
+    b_row = sb / BPR;
+    b_col8 = (sb % BPR) ^ (G::b_swizzle(b_row) >> 1);  // b_swizzle counts 4-value chunks
+    a_off = 2u * ((uint32_t)a_row * (uint32_t)p.lda + (uint32_t)(8 * a_col8));
+    b_off = 2u * ((uint32_t)b_row * (uint32_t)p.ldb + (uint32_t)(8 * b_col8));
+    a_step = 2u * (uint32_t)A_ROWS_STEP * (uint32_t)p.lda;
+    b_step = 2u * (uint32_t)B_ROWS_STEP * (uint32_t)p.ldb;
+    last_stage = (p.k - 1) / G::BK;
+    a_last = p.k > 0 ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
+    b_last = p.k > 0 ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
+  }
+
+  // Issues the loads of stage kt into LDS buffer `stage` (a stage's first element).
+  __device__ __forceinline__ void issue(int kt, uint16_t* stage) const {
+    const uint32_t base = lds_address(stage) + 2u * (uint32_t)(wave * kWave * 8);
+    const uint32_t a_n = (uint32_t)(a_bytes < 0 ? 0 : (a_bytes > 0xffffffffll ? 0xffffffffll : a_bytes));
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      load_to_lds16(a_tile, a_n, base + 2u * (uint32_t)(i * WAVES * kWave * 8), a_off,
+                    2u * G::BK * (uint32_t)kt + i * a_step);
+    }
+    const int64_t skip = 2 * (int64_t)G::BK * kt * ldb;
+    const int64_t b_left = b_bytes - skip;
+    const uint32_t b_n = (uint32_t)(b_left < 0 ? 0 : (b_left > 0xffffffffll ? 0xffffffffll : b_left));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      load_to_lds16(b_tile + skip / 2, b_n, base + 2u * (uint32_t)(G::A_STAGE + i * WAVES * kWave * 8), b_off,
+                    i * b_step);
+    }
+  }
+
+  // Repairs this thread's pieces of stage kt (the one that holds k = K - 1)
+  // in LDS buffer `stage`, after their loads have landed: A values at k >= K
+  // and B rows at k >= K become zero, and the matrices' last values are put
+  // back where a straddling dword read them as zero.
+  __device__ __forceinline__ void fix_last_stage(int kt, uint16_t* stage) const {
+    const int lane = opaque_tid() & (kWave - 1);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      u32x4_t* slot = reinterpret_cast<u32x4_t*>(stage + (i * WAVES + wave) * (kWave * 8) + 8 * lane);
+      const int col = kt * G::BK + 8 * a_col8;
+      const int row = m0 + a_row + i * A_ROWS_STEP;
+      u32x4_t val = keep_values(*slot, k - col);
+      val = put_value(val, row == m - 1 ? k - 1 - col : -1, a_last);
+      *slot = val;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      u32x4_t* slot = reinterpret_cast<u32x4_t*>(stage + G::A_STAGE + (i * WAVES + wave) * (kWave * 8) + 8 * lane);
+      const int krow = kt * G::BK + b_row + i * B_ROWS_STEP;
+      const int col = n0 + 8 * b_col8;
+      const u32x4_t zero = {0u, 0u, 0u, 0u};
+      u32x4_t val = krow < k ? *slot : zero;
+      val = put_value(val, krow == k - 1 ? n - 1 - col : -1, b_last);
+      *slot = val;
+    }
+  }
+};
+
+// Waits until at most `n` vector-memory operations of this wave are in flight
+// (other counters unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier that waits for this wave's LDS accesses (lgkmcnt 0) but
+// not for its global loads: the caller waits for the loads it needs first.
+// The empty asm keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // D = alpha * acc + beta * C for one element; C is read only when c != nullptr
 // and beta != 0 (src/grouped_gemm.cu:475-479, 616-621).

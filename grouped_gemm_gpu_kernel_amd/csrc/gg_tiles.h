@@ -55,6 +55,45 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
   }
 }
 
+// The k-loop with stage loads straight into LDS (32-bit offsets): BUFFERS
+// LDS buffers, BUFFERS - 1 stages in flight.  While stage k is multiplied out
+// of buffer k % BUFFERS, the loads of stage k + BUFFERS - 1 go to the buffer
+// every wave finished multiplying in the previous step; each wave then waits
+// until its own loads of stage k + 1 have landed (the stage holding K - 1 is
+// repaired then), and a barrier without a memory fence closes the step -- a
+// fenced barrier would also wait for the stages still in flight.  Loads are
+// issued for stages past K too (they read as zero or land unread).
+template <class G, class Compute>
+__device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
+                                               Compute&& compute) {
+  constexpr int NBUF = G::BUFFERS;
+  constexpr int L = NBUF - 1;
+  constexpr int PENDING = (L - 1) * DmaLoader<G>::LOADS;  // loads of later stages allowed in flight
+  const int nk = (p.k + G::BK - 1) / G::BK;
+  if (nk <= 0) return;
+  const DmaLoader<G> loader(p, m0, n0);
+#pragma unroll
+  for (int s = 0; s < L; ++s) loader.issue(s, lds + s * G::STAGE);
+  wait_vmcnt<PENDING>();
+  if (loader.last_stage == 0) loader.fix_last_stage(0, lds);
+  stage_barrier();
+  // One step per iteration, not unrolled: no register set has to be indexed
+  // statically, and one copy of the step keeps the code a launch has to fetch
+  // into a cold instruction cache small.  u is the buffer of stage k.
+  int u = 0;
+#pragma unroll 1
+  for (int k = 0; k < nk; ++k) {
+    const int ul = u == 0 ? L : u - 1;  // (u + L) % NBUF
+    const int un = u == NBUF - 1 ? 0 : u + 1;
+    loader.issue(k + L, lds + ul * G::STAGE);
+    compute(lds + u * G::STAGE);
+    wait_vmcnt<PENDING>();
+    if (k + 1 == loader.last_stage) loader.fix_last_stage(k + 1, lds + un * G::STAGE);
+    stage_barrier();
+    u = un;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // MFMA tile: v_mfma_f32_32x32x16_f16, (BM/64) x (BN/64) waves, each owning a
 // 64 x 64 block of D held as 2 x 2 32x32 accumulators.
@@ -96,7 +135,7 @@ struct MfmaTile {
       half8_t bf[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const uint16_t* src = as + (wm * WM + fm * 32 + (lane & 31)) * G::SA + s * 16 + (lane >> 5) * 8;
+        const uint16_t* src = as + G::a_piece(wm * WM + fm * 32 + (lane & 31), 2 * s + (lane >> 5));
         af[fm] = *reinterpret_cast<const half8_t*>(src);
       }
 #pragma unroll
@@ -139,9 +178,14 @@ struct MfmaTile {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[fm][fn][e] = 0.0f;
 
-    run_k_loop<G, WIDE>(p, m0, n0, lds, [&](const uint16_t* stage) {
+    auto compute = [&](const uint16_t* stage) {
       if (live) compute_stage(stage, lane, wm, wn, acc);
-    });
+    };
+    if constexpr (WIDE) {
+      run_k_loop<G, WIDE>(p, m0, n0, lds, compute);
+    } else {
+      run_k_loop_dma<G>(p, m0, n0, lds, compute);
+    }
 
     if (!live) return;
     store_tile<WIDE>(p, m0 + wm * WM, n0 + wn * WN, lane, acc);
@@ -291,7 +335,7 @@ struct FmaTile {
       half8_t av[RM];
 #pragma unroll
       for (int i = 0; i < RM; ++i) {
-        av[i] = *reinterpret_cast<const half8_t*>(as + (tm * RM + i) * G::SA + k8 * 8);
+        av[i] = *reinterpret_cast<const half8_t*>(as + G::a_piece(tm * RM + i, k8));
       }
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {

@@ -28,8 +28,9 @@ GGK_KERNEL_GROUPED = 0
 GGK_KERNEL_SINGLE = 1
 GGK_ADDR_32 = 0
 GGK_ADDR_64 = 1
-GGK_SCHEDULER_STATE_INTS = 16
 GGK_SCHEDULER_CHUNKS = 8
+GGK_SCHEDULER_COUNTER_STRIDE = 32
+GGK_SCHEDULER_STATE_INTS = GGK_SCHEDULER_COUNTER_STRIDE * (GGK_SCHEDULER_CHUNKS + 1)
 GGK_MOE_MAX_EXPERTS = 1024
 GGK_MOE_HEADER_INTS = 16
 GGK_MOE_STATUS = 12

@@ -46,6 +46,8 @@ __device__ __forceinline__ gg_device_problem_desc load_problem(const gg_device_p
 }
 
 constexpr int kChunks = GGK_SCHEDULER_CHUNKS;  // one per XCD
+constexpr int kStride = GGK_SCHEDULER_COUNTER_STRIDE;
+static_assert((kChunks & (kChunks - 1)) == 0 && kChunks <= kWave, "chunks are a power of two, one lane each");
 
 struct GroupedArgs {
   const gg_device_problem_desc* __restrict__ problems;
@@ -53,7 +55,7 @@ struct GroupedArgs {
   const int* __restrict__ work_offsets;  // work tiles: [count + 1]
   int count;
   int total;           // work tiles
-  int* state;          // [0, kChunks) chunk claim counters, [kChunks] retired workgroups
+  int* state;          // chunk c's claim counter at [c * kStride], retired workgroups at [kChunks * kStride]
   int* tile_map;       // traced launches only
   long long* wg_clock; // traced launches only
   int bounds[kChunks + 1];  // chunk c owns work-tile indices [bounds[c], bounds[c + 1])
@@ -63,21 +65,69 @@ struct GroupedArgs {
   const int* header;
 };
 
-// Claims the next work-tile index for the calling workgroup (one thread calls it).
-// Workgroups are dispatched to the XCDs round-robin, so workgroup w runs on
-// XCD w % kChunks and starts on that chunk: the tiles of one problem, which
-// share A and B panels, are then multiplied on one XCD and its L2 serves the
-// re-reads.  When a chunk runs dry the workgroup moves on to the next one
-// (stealing); `visit` counts the chunks it has left behind.  Returns total
-// when every chunk is exhausted.
-__device__ __forceinline__ int claim_tile(const GroupedArgs& args, const int* bounds, int total, int home,
-                                          int& visit) {
+// Scheduling.  Workgroups are dispatched to the XCDs round-robin, so
+// workgroup w runs on XCD w % kChunks and starts on that chunk (its home):
+// the tiles of one problem, which share A and B panels, are then multiplied
+// on one XCD and its L2 serves the re-reads.  Workgroup w's first tile is
+// fixed, index bounds[home] + w / kChunks, so a launch starts without any
+// counter traffic; the rest of chunk c, [bounds[c] + fixed_slots(c),
+// bounds[c + 1]), is handed out one index per atomicAdd on the chunk's
+// counter.  A counter request takes microseconds (device-scope atomics are
+// resolved past the XCDs' L2s), so it is made while the current tile is being
+// computed and read after it.  When a chunk runs dry the workgroup moves on
+// to the next one (stealing); `visit` counts the chunks it has left behind,
+// in the order home, home + 1, ... (mod kChunks).  All claim logic runs in
+// wave 0, uniformly; lane 0 makes the requests.
+
+// Workgroups whose first tile is fixed in chunk c.
+__device__ __forceinline__ int fixed_slots(int c, int grid) {
+  return c < grid ? (grid - 1 - c) / kChunks + 1 : 0;
+}
+
+// First index of chunk c handed out by its counter.
+__device__ __forceinline__ int counted_from(const int* bounds, int c, int grid) {
+  return bounds[c] + fixed_slots(c, grid);
+}
+
+// The first visit at or after `visit` whose chunk has indices for its counter
+// to hand out (kChunks if none).
+__device__ __forceinline__ int first_counted(const int* bounds, int grid, int home, int visit) {
+  for (; visit < kChunks; ++visit) {
+    const int c = (home + visit) & (kChunks - 1);
+    if (counted_from(bounds, c, grid) < bounds[c + 1]) break;
+  }
+  return visit;
+}
+
+// Claims an index now (wave 0): one lane per remaining chunk reads that
+// chunk's counter, the first chunk with indices left is asked, and the search
+// goes on past it if the request comes back empty.  Counters only grow
+// during a launch, so a chunk read as dry stays dry.  Returns total, with
+// visit = kChunks, when every chunk is exhausted.
+__device__ __forceinline__ int claim_now(int* state, const int* bounds, int grid, int home, int& visit, int total) {
+  const int lane = threadIdx.x & (kWave - 1);
   while (visit < kChunks) {
-    const int c = (home + visit) % kChunks;
-    const int t = bounds[c] + atomicAdd(args.state + c, 1);
+    bool open = false;
+    const int v = visit + lane;
+    if (v < kChunks) {
+      const int c = (home + v) & (kChunks - 1);
+      const int from = counted_from(bounds, c, grid);
+      const int end = bounds[c + 1];
+      if (from < end) {
+        open = from + __hip_atomic_load(state + c * kStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < end;
+      }
+    }
+    const uint64_t found = __ballot(open);
+    if (found == 0) break;
+    visit += __builtin_ctzll(found);
+    const int c = (home + visit) & (kChunks - 1);
+    int got = 0;
+    if (lane == 0) got = atomicAdd(state + c * kStride, 1);
+    const int t = counted_from(bounds, c, grid) + __builtin_amdgcn_readfirstlane(got);
     if (t < bounds[c + 1]) return t;
     ++visit;
   }
+  visit = kChunks;
   return total;
 }
 
@@ -146,10 +196,12 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
   using G = typename S::G;
   using Tile = typename TileFor<PATH, G>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
-  __shared__ int s_claim;
+  __shared__ int s_claim[2];
   __shared__ int s_schedule[kChunks + 2];
 
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const bool wave0 = __builtin_amdgcn_readfirstlane(tid / kWave) == 0;
   long long clock_start = 0;
   long long clock_end = 0;
   if (TRACED) {
@@ -157,18 +209,44 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
     clock_end = clock_start;
   }
 
+  const int grid = gridDim.x;
   const int home = blockIdx.x % kChunks;
-  int visit = 0;  // meaningful in thread 0 only
-  int next = 0;
   load_schedule(args, s_schedule);
   __syncthreads();
   const int total = __builtin_amdgcn_readfirstlane(s_schedule[kChunks + 1]);
-  if (tid == 0) s_claim = claim_tile(args, s_schedule, total, home, visit);
-  __syncthreads();
-  int t = __builtin_amdgcn_readfirstlane(s_claim);
+  // Whether any chunk has indices beyond the fixed first tiles: when none has,
+  // no counter is touched and none needs resetting.
+  const bool counted = first_counted(s_schedule, grid, 0, 0) < kChunks;
+
+  int visit = 0;  // wave 0
+  int t = __builtin_amdgcn_readfirstlane(s_schedule[home] + (int)blockIdx.x / kChunks);
+  int parity = 0;
+  if (t >= __builtin_amdgcn_readfirstlane(s_schedule[home + 1])) {
+    // No fixed tile for this workgroup (its chunk is smaller than its share
+    // of the grid): claim one now.
+    if (wave0) {
+      const int c = counted ? claim_now(args.state, s_schedule, grid, home, visit, total) : total;
+      if (lane == 0) s_claim[0] = c;
+    }
+    __syncthreads();
+    t = __builtin_amdgcn_readfirstlane(s_claim[0]);
+    parity = 1;
+  }
+
   while (t < total) {
-    // Claim the next index now; its latency hides behind this tile's work.
-    if (tid == 0) next = claim_tile(args, s_schedule, total, home, visit);
+    // The request for the next index, made once while this tile is computed.
+    bool asked = false;
+    int chunk = -1;  // wave 0: the chunk asked, -1 if none
+    int got = 0;     // wave 0, lane 0: what the request returned
+    auto request = [&]() -> bool {
+      asked = true;
+      if (!wave0 || !counted) return false;
+      visit = first_counted(s_schedule, grid, home, visit);
+      if (visit >= kChunks) return false;
+      chunk = (home + visit) & (kChunks - 1);
+      if (lane == 0) got = atomicAdd(args.state + chunk * kStride, 1);
+      return true;
+    };
 
     const int prob = find_problem(args.work_offsets, args.count, t);
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
@@ -194,16 +272,28 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
             }
           }
         } else {
-          Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds);
+          Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
         }
       }
     }
+    if (!asked) request();
     if (TRACED) clock_end = wall_clock64();
 
-    __syncthreads();  // every thread has read s_claim for this round
-    if (tid == 0) s_claim = next;
+    if (wave0) {
+      int next = total;
+      if (chunk >= 0) {
+        next = counted_from(s_schedule, chunk, grid) + __builtin_amdgcn_readfirstlane(got);
+        if (next >= s_schedule[chunk + 1]) {
+          ++visit;
+          next = claim_now(args.state, s_schedule, grid, home, visit, total);
+        }
+      }
+      // Slot `parity` was last read before the previous barrier.
+      if (lane == 0) s_claim[parity] = next;
+    }
     __syncthreads();
-    t = __builtin_amdgcn_readfirstlane(s_claim);
+    t = __builtin_amdgcn_readfirstlane(s_claim[parity]);
+    parity ^= 1;
   }
 
   if (tid == 0) {
@@ -211,12 +301,15 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       args.wg_clock[2 * blockIdx.x + 0] = clock_start;
       args.wg_clock[2 * blockIdx.x + 1] = clock_end;
     }
-    // A workgroup retires only after a failed claim on every chunk, so when
-    // the last one retires no claim is in flight: it returns the counters to
-    // zero for the next launch in stream order.
-    const int retired = atomicAdd(args.state + kChunks, 1);
-    if (retired == (int)gridDim.x - 1) {
-      for (int c = 0; c <= kChunks; ++c) atomicExch(args.state + c, 0);
+    // A workgroup leaves only after finding every chunk exhausted, with no
+    // request in flight, so when the last one leaves nobody will touch the
+    // counters again: it returns them to zero for the next launch in stream
+    // order.
+    if (counted) {
+      const int retired = atomicAdd(args.state + kChunks * kStride, 1);
+      if (retired == grid - 1) {
+        for (int c = 0; c <= kChunks; ++c) atomicExch(args.state + c * kStride, 0);
+      }
     }
   }
 }
@@ -233,7 +326,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_single_kernel(gg_device_problem_desc
   if (wtn <= 0 || t >= wtm * wtn) return;
   const int wm = t / wtn;
   const int wn = t - wm * wtn;
-  Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds);
+  Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, [] { return false; });
 }
 
 // ---------------------------------------------------------------------------

@@ -13,7 +13,11 @@
 namespace gg {
 
 // Runs the staged k-loop of one tile: compute(stage_pointer) is called once
-// per stage with that stage's LDS buffer.
+// per stage with that stage's LDS buffer, and on_start() once, by every
+// thread, after the first loads are on their way (the persistent scheduler
+// requests its next tile there, so that the request's latency overlaps this
+// tile's).  on_start returns whether the calling wave issued one global
+// memory request of its own.
 //
 // Stage s is fetched into register set s % DEPTH.  While stage k is
 // multiplied out of LDS buffer k % 2, the loads of stage k + DEPTH - 1 are
@@ -26,16 +30,20 @@ namespace gg {
 // runs whole groups of DEPTH steps with no branch; the last steps of a tile
 // are guarded.  The body is unrolled DEPTH times so that every register set
 // is addressed statically.
-template <class G, bool WIDE, class Compute>
+template <class G, bool WIDE, class Compute, class OnStart>
 __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                           Compute&& compute) {
+                                           Compute&& compute, OnStart&& on_start) {
   constexpr int D = G::DEPTH;
   const int nk = (p.k + G::BK - 1) / G::BK;
-  if (nk <= 0) return;
+  if (nk <= 0) {
+    on_start();
+    return;
+  }
   const StageLoader<G, WIDE> loader(p, m0, n0);
   RawStage<G, WIDE> ring[D];
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) loader.issue(s, ring[s]);
+  on_start();  // the compiler's waits count the request like any other load
   loader.store(ring[0], 0, lds, 0);
   __syncthreads();
   auto step = [&](int k, int u) {
@@ -63,14 +71,23 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
 // repaired then), and a barrier without a memory fence closes the step -- a
 // fenced barrier would also wait for the stages still in flight.  Loads are
 // issued for stages past K too (they read as zero or land unread).
-template <class G, class Compute>
+//
+// on_start runs in the first step, after the loads of stage L are issued: a
+// request it makes is then the youngest in flight, and the first step's wait
+// lets it stay in flight (loads complete in order, so one more outstanding
+// operation is exactly that request).  The second step's wait retires it, so
+// it has two stage computations to come back.
+template <class G, class Compute, class OnStart>
 __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                               Compute&& compute) {
+                                               Compute&& compute, OnStart&& on_start) {
   constexpr int NBUF = G::BUFFERS;
   constexpr int L = NBUF - 1;
   constexpr int PENDING = (L - 1) * DmaLoader<G>::LOADS;  // loads of later stages allowed in flight
   const int nk = (p.k + G::BK - 1) / G::BK;
-  if (nk <= 0) return;
+  if (nk <= 0) {
+    on_start();
+    return;
+  }
   const DmaLoader<G> loader(p, m0, n0);
 #pragma unroll
   for (int s = 0; s < L; ++s) loader.issue(s, lds + s * G::STAGE);
@@ -86,8 +103,13 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
     const int ul = u == 0 ? L : u - 1;  // (u + L) % NBUF
     const int un = u == NBUF - 1 ? 0 : u + 1;
     loader.issue(k + L, lds + ul * G::STAGE);
+    const bool extra = k == 0 && __builtin_amdgcn_readfirstlane(on_start() ? 1 : 0) != 0;
     compute(lds + u * G::STAGE);
-    wait_vmcnt<PENDING>();
+    if (extra) {
+      wait_vmcnt<PENDING + 1>();
+    } else {
+      wait_vmcnt<PENDING>();
+    }
     if (k + 1 == loader.last_stage) loader.fix_last_stage(k + 1, lds + un * G::STAGE);
     stage_barrier();
     u = un;
@@ -158,9 +180,10 @@ struct MfmaTile {
     }
   }
 
-  // Computes the work tile at (m0, n0).
-  template <bool WIDE>
-  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds) {
+  // Computes the work tile at (m0, n0); on_start as in the k-loops.
+  template <bool WIDE, class OnStart>
+  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
+                                             OnStart&& on_start) {
     const int tid = opaque_tid();
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -182,9 +205,9 @@ struct MfmaTile {
       if (live) compute_stage(stage, lane, wm, wn, acc);
     };
     if constexpr (WIDE) {
-      run_k_loop<G, WIDE>(p, m0, n0, lds, compute);
+      run_k_loop<G, WIDE>(p, m0, n0, lds, compute, on_start);
     } else {
-      run_k_loop_dma<G>(p, m0, n0, lds, compute);
+      run_k_loop_dma<G>(p, m0, n0, lds, compute, on_start);
     }
 
     if (!live) return;
@@ -360,9 +383,10 @@ struct FmaTile {
     }
   }
 
-  // Computes the work tile at (m0, n0).
-  template <bool WIDE>
-  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds) {
+  // Computes the work tile at (m0, n0); on_start as in the k-loops.
+  template <bool WIDE, class OnStart>
+  __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
+                                             OnStart&& on_start) {
     const int tid = threadIdx.x;
     const int tm = tid >> 4;
     const int tn = tid & 15;
@@ -379,7 +403,7 @@ struct FmaTile {
     run_k_loop<G, WIDE>(p, m0, n0, lds, [&](const uint16_t* stage) {
       if (active) compute_stage(stage, p.k - kt * G::BK, tm, tn, acc);
       ++kt;
-    });
+    }, on_start);
 
     if (!active) return;
     const bool use_c = p.c != nullptr && p.beta != 0.0f;

@@ -62,14 +62,20 @@ enum { GGK_KERNEL_GROUPED = 0, GGK_KERNEL_SINGLE = 1 };
 
 /* The persistent grid claims tiles from GGK_SCHEDULER_CHUNKS contiguous
  * chunks of the tile index range, one per XCD (an MI355X has 8); workgroup w
- * starts on chunk w % GGK_SCHEDULER_CHUNKS and moves to the next chunk when
- * its own is exhausted. */
+ * starts on chunk w % GGK_SCHEDULER_CHUNKS -- its first tile there is fixed by
+ * w, later ones are claimed from the chunk's counter -- and moves to the next
+ * chunk when its own is exhausted. */
 #define GGK_SCHEDULER_CHUNKS 8
 
-/* Ints of scheduler state one grouped launch needs: a claim counter per chunk,
- * a retire counter, spares.  Must be zero before the first launch; every
- * launch leaves it zero again when its last workgroup retires. */
-#define GGK_SCHEDULER_STATE_INTS 16
+/* Ints between two scheduler counters: each sits on a 128-byte line of its
+ * own, so the workgroups claiming from different chunks do not queue on one
+ * line. */
+#define GGK_SCHEDULER_COUNTER_STRIDE 32
+
+/* Ints of scheduler state one grouped launch needs: a claim counter per chunk
+ * and a retire counter, GGK_SCHEDULER_COUNTER_STRIDE apart.  Must be zero
+ * before the first launch; every launch leaves it zero again. */
+#define GGK_SCHEDULER_STATE_INTS (GGK_SCHEDULER_COUNTER_STRIDE * (GGK_SCHEDULER_CHUNKS + 1))
 
 typedef struct ggk_device_info {
   int device;

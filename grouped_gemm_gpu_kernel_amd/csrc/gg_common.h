@@ -115,38 +115,59 @@ template <> struct VariantTile<GGK_VARIANT_64x64x16> { static constexpr int M = 
 template <> struct VariantTile<GGK_VARIANT_128x64x32> { static constexpr int M = 128, N = 64; };
 template <> struct VariantTile<GGK_VARIANT_64x128x32> { static constexpr int M = 64, N = 128; };
 
-// Kernel shape of (variant, path).  The MFMA path computes a 2 x 2 block of
-// reference tiles per claim with one wave per 64 x 64 block of D: each A and B
-// value fetched from L2 feeds twice the multiply-adds it would feed in a
-// single reference tile, which halves the L2 -> CU traffic that bounds these
-// kernels.  The FMA path computes one reference tile with 256 threads.
+// Kernel shape of (variant, path).  The MFMA path computes a block of TM x TN
+// reference tiles per claim: each A and B value fetched from L2 then feeds TN
+// (A) or TM (B) times the multiply-adds it would feed in a single reference
+// tile, which cuts the L2 -> CU traffic that bounds these kernels, and each
+// wave owns a WAVE_M x WAVE_N block of D, so that every operand fragment it
+// reads from LDS feeds several MFMAs.  128x64x32 (the configuration the
+// reference benchmarks by default): 2 x 4 tiles = 256 x 256 of D, eight waves
+// of 128 x 64.  64x64x16 and 64x128x32: 2 x 2 tiles, waves of 64 x 64.  The
+// FMA path computes one reference tile with 256 threads.
 template <int V, int PATH> struct KernelShape;
 #ifndef GG_WORK_TM
 #define GG_WORK_TM 2
 #endif
 #ifndef GG_WORK_TN
-#define GG_WORK_TN 2
+#define GG_WORK_TN 4
 #endif
 #ifndef GG_WAVE_N
 #define GG_WAVE_N 64
 #endif
+#ifndef GG_WAVE_M
+#define GG_WAVE_M 128
+#endif
+#ifndef GG_TUNED_WAVES_PER_EU
+#define GG_TUNED_WAVES_PER_EU 2
+#endif
+#ifndef GG_DMA_BUFFERS
+#define GG_DMA_BUFFERS 0  // 0: see KernelShape::BUFFERS
+#endif
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
-  // GG_WORK_TM / GG_WORK_TN / GG_WAVE_N retune the 128x64x32 variant only.
+  // The GG_* shape macros retune the 128x64x32 variant only.
   static constexpr bool kTuned = V == GGK_VARIANT_128x64x32;
   static constexpr int TM = kTuned ? GG_WORK_TM : 2;  // reference tiles per work tile, along M
   static constexpr int TN = kTuned ? GG_WORK_TN : 2;  // and along N
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
   static constexpr int WAVE_N = kTuned && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave
-  static constexpr int THREADS = (BM / 64) * (BN / WAVE_N) * kWave;
-  // Stages load straight into LDS: three buffers (two stages in flight) for the
-  // 512-thread tiles, which have a CU to themselves; two for the 256-thread
-  // tile, so that two of its workgroups share a CU.
-  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, THREADS, THREADS >= 512 ? 3 : 2, true>;
+  static constexpr int WAVE_M = kTuned && GG_WAVE_M < BM ? GG_WAVE_M : 64;                    // rows of D per wave
+  static constexpr int THREADS = (BM / WAVE_M) * (BN / WAVE_N) * kWave;
+  // Waves each SIMD must be able to hold (bounds the registers per lane).
+  static constexpr int WAVES_PER_EU = kTuned ? GG_TUNED_WAVES_PER_EU : 2;
+  // Stages load straight into LDS.  A 512-thread workgroup has a CU to
+  // itself and takes three buffers (two stages in flight) when they fit in
+  // LDS, else two; a 256-thread one takes two, so that two of its workgroups
+  // share a CU.
+  static constexpr int STAGE_BYTES = 2 * GG_STAGE_K * (BM + BN);
+  static constexpr int BUFFERS =
+      GG_DMA_BUFFERS > 0 ? GG_DMA_BUFFERS : (THREADS >= 512 && 3 * STAGE_BYTES <= 150 * 1024 ? 3 : 2);
+  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, THREADS, BUFFERS, true>;
 };
 template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr int TM = 1;
   static constexpr int TN = 1;
+  static constexpr int WAVES_PER_EU = 2;
   using G = Geometry<VariantTile<V>::M, VariantTile<V>::N, GG_STAGE_K, GG_STAGE_DEPTH, 256>;
 };
 
@@ -562,6 +583,9 @@ struct DmaLoader {
     b_col8 = (sb % BPR) ^ (G::b_swizzle(b_row) >> 1);  // b_swizzle counts 4-value chunks
     a_off = 2u * ((uint32_t)a_row * (uint32_t)p.lda + (uint32_t)(8 * a_col8));
     b_off = 2u * ((uint32_t)b_row * (uint32_t)p.ldb + (uint32_t)(8 * b_col8));
+    // A thread's B pieces all start at column n0 + 8 b_col8; past N they only
+    // feed columns of D that are never stored, so they are not fetched.
+    if (n0 + 8 * b_col8 >= p.n) b_off = kOutOfRange;
     a_step = 2u * (uint32_t)A_ROWS_STEP * (uint32_t)p.lda;
     b_step = 2u * (uint32_t)B_ROWS_STEP * (uint32_t)p.ldb;
     last_stage = (p.k - 1) / G::BK;
@@ -569,18 +593,28 @@ struct DmaLoader {
     b_last = p.k > 0 ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
   }
 
+  // Byte offset no load reaches: the 32-bit addressing form keeps every
+  // offset a tile reads below 2^31, so record counts are capped there and an
+  // offset of 2^31 (plus any soffset) reads zeros without touching memory.
+  static constexpr uint32_t kOutOfRange = 0x80000000u;
+  __device__ static __forceinline__ uint32_t records(int64_t bytes) {
+    return (uint32_t)(bytes < 0 ? 0 : (bytes > (int64_t)kOutOfRange ? (int64_t)kOutOfRange : bytes));
+  }
+
   // Issues the loads of stage kt into LDS buffer `stage` (a stage's first element).
   __device__ __forceinline__ void issue(int kt, uint16_t* stage) const {
     const uint32_t base = lds_address(stage) + 2u * (uint32_t)(wave * kWave * 8);
-    const uint32_t a_n = (uint32_t)(a_bytes < 0 ? 0 : (a_bytes > 0xffffffffll ? 0xffffffffll : a_bytes));
+    const uint32_t a_n = records(a_bytes);
+    // A pieces that start at k >= K are zero in the product; they are not
+    // fetched (the piece that straddles K is, and is repaired afterwards).
+    const uint32_t a_voff = kt * G::BK + 8 * a_col8 < k ? a_off : kOutOfRange;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      load_to_lds16(a_tile, a_n, base + 2u * (uint32_t)(i * WAVES * kWave * 8), a_off,
+      load_to_lds16(a_tile, a_n, base + 2u * (uint32_t)(i * WAVES * kWave * 8), a_voff,
                     2u * G::BK * (uint32_t)kt + i * a_step);
     }
     const int64_t skip = 2 * (int64_t)G::BK * kt * ldb;
-    const int64_t b_left = b_bytes - skip;
-    const uint32_t b_n = (uint32_t)(b_left < 0 ? 0 : (b_left > 0xffffffffll ? 0xffffffffll : b_left));
+    const uint32_t b_n = records(b_bytes - skip);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       load_to_lds16(b_tile + skip / 2, b_n, base + 2u * (uint32_t)(G::A_STAGE + i * WAVES * kWave * 8), b_off,

@@ -182,19 +182,17 @@ __device__ __forceinline__ int work_tiles_n(const gg_device_problem_desc& p) {
   return (p.tiles_n + TN - 1) / TN;
 }
 
-// At least GG_WAVES_PER_EU waves per SIMD: 2 allows 256 VGPRs + AGPRs per lane
-// (a 512-thread workgroup, or two 256-thread ones).
-#ifndef GG_WAVES_PER_EU
-#define GG_WAVES_PER_EU 2
-#endif
-#define GG_KERNEL_ATTRS(V, PATH) \
-  __launch_bounds__((KernelShape<V, PATH>::G::THREADS)) __attribute__((amdgpu_waves_per_eu(GG_WAVES_PER_EU)))
+// At least KernelShape::WAVES_PER_EU waves per SIMD: 2 allows 256 VGPRs +
+// AGPRs per lane (a 512-thread workgroup, or two 256-thread ones), 1 allows 512.
+#define GG_KERNEL_ATTRS(V, PATH)                          \
+  __launch_bounds__((KernelShape<V, PATH>::G::THREADS)) \
+      __attribute__((amdgpu_waves_per_eu(KernelShape<V, PATH>::WAVES_PER_EU)))
 
 template <int V, int PATH, bool TRACED, bool WIDE>
 __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
   using S = KernelShape<V, PATH>;
   using G = typename S::G;
-  using Tile = typename TileFor<PATH, G>::type;
+  using Tile = typename TileFor<S, PATH>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
   __shared__ int s_claim[2];
   __shared__ int s_schedule[kChunks + 2];
@@ -318,7 +316,7 @@ template <int V, int PATH, bool WIDE>
 __global__ GG_KERNEL_ATTRS(V, PATH) void gg_single_kernel(gg_device_problem_desc p) {
   using S = KernelShape<V, PATH>;
   using G = typename S::G;
-  using Tile = typename TileFor<PATH, G>::type;
+  using Tile = typename TileFor<S, PATH>::type;
   __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
   const int t = blockIdx.x;
   const int wtn = work_tiles_n<S::TM, S::TN>(p);
@@ -535,15 +533,18 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
 }
 
 // 32-bit offsets from a work tile's origin reach every A and B value the
-// tile reads when 0 <= lda, 0 <= ldb, BM * lda < 2^30 and BK * ldb < 2^30;
+// tile reads when 0 <= lda, 0 <= ldb, BM * lda + K + 8 BK < 2^30 and
+// BK * ldb < 2^30 (elements; the loader also requests a few stages past K);
 // the epilogue's per-lane offsets (a few rows of C or D) when 0 <= ldc, ldd
-// < 2^27 (ldc only matters when C is read).
+// < 2^27 (ldc only matters when C is read).  Every byte offset then stays
+// below 2^31, which the loader's out-of-range marker relies on.
 static bool fits_addr32(const KernelSet& k, const gg_device_problem_desc& p) {
   constexpr int64_t kLimit = int64_t(1) << 30;
   constexpr int64_t kLdLimit = int64_t(1) << 27;
   const bool reads_c = p.c != nullptr && p.beta != 0.0f;
-  return p.lda >= 0 && p.ldb >= 0 && (int64_t)k.bm * p.lda < kLimit && (int64_t)k.bk * p.ldb < kLimit &&
-         p.ldd >= 0 && p.ldd < kLdLimit && (!reads_c || (p.ldc >= 0 && p.ldc < kLdLimit));
+  return p.lda >= 0 && p.ldb >= 0 && p.k >= 0 && (int64_t)k.bm * p.lda + p.k + 8 * k.bk < kLimit &&
+         (int64_t)k.bk * p.ldb < kLimit && p.ldd >= 0 && p.ldd < kLdLimit &&
+         (!reads_c || (p.ldc >= 0 && p.ldc < kLdLimit));
 }
 
 hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out) {

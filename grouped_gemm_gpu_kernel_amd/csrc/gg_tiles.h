@@ -117,8 +117,8 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
 }
 
 // ---------------------------------------------------------------------------
-// MFMA tile: v_mfma_f32_32x32x16_f16, (BM/64) x (BN/64) waves, each owning a
-// 64 x 64 block of D held as 2 x 2 32x32 accumulators.
+// MFMA tile: v_mfma_f32_32x32x16_f16, (BM/WM) x (BN/WN) waves, each owning a
+// WM x WN block of D held as (WM/32) x (WN/32) 32x32 accumulators.
 //
 // Operand layouts of v_mfma_f32_32x32x16_f16 (lane l of 64):
 //   A: row l%32, k = 8*(l/32) + e, e = 0..7 (one 16-byte read of an A row)
@@ -131,9 +131,9 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
 // addresses row kb + j/4, columns nb + 4*(j%4), and lane i receives
 // B[kb + e][nb + i].
 // ---------------------------------------------------------------------------
-template <class G>
+template <class G, int WM_>
 struct MfmaTile {
-  static constexpr int WM = 64;
+  static constexpr int WM = WM_;
   static constexpr int WAVES_M = G::BM / WM;
   static constexpr int WAVES_N = G::THREADS / kWave / WAVES_M;
   static constexpr int WN = G::BN / WAVES_N;
@@ -141,6 +141,11 @@ struct MfmaTile {
   static constexpr int FN = WN / 32;
   static_assert(WAVES_M * WAVES_N * kWave == G::THREADS, "one wave per block of D");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must hold whole 32x32 blocks");
+  // 32-row groups of D per epilogue chunk: the whole block for blocks of up
+  // to 2 x 2 accumulators (16 C vectors, 64 registers), one row of
+  // accumulators per chunk for larger blocks, which hold more registers.
+  static constexpr int EPI_ROWS = FM * FN <= 4 ? FM : 1;
+  static_assert(FM % EPI_ROWS == 0, "whole chunks");
 
   // Multiplies one LDS stage into acc.  All MFMAs of a stage are issued
   // unconditionally; skipping is decided once per tile for the whole wave.
@@ -151,10 +156,8 @@ struct MfmaTile {
     lane = opaque_tid() & (kWave - 1);
     const int g = lane >> 4;
     const int j = lane & 15;
-#pragma unroll
-    for (int s = 0; s < G::BK / 16; ++s) {
-      half8_t af[FM];
-      half8_t bf[FN];
+    // Operand fragments of k-step s (16 deep) of the stage.
+    auto load_frags = [&](int s, half8_t (&af)[FM], half8_t (&bf)[FN]) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         const uint16_t* src = as + G::a_piece(wm * WM + fm * 32 + (lane & 31), 2 * s + (lane >> 5));
@@ -170,12 +173,38 @@ struct MfmaTile {
         const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GG_LDS short4_t*)(src + 4 * G::SB));
         bf[fn] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
+    };
+    auto multiply = [&](const half8_t (&af)[FM], const half8_t (&bf)[FN]) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
         }
+      }
+    };
+    constexpr int STEPS = G::BK / 16;
+    if constexpr (FM * FN <= 4) {
+      // Small wave blocks: the compiler may schedule the whole stage freely.
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) {
+        half8_t af[FM];
+        half8_t bf[FN];
+        load_frags(s, af, bf);
+        multiply(af, bf);
+      }
+    } else {
+      // Large wave blocks: fragments of step s + 1 are read while step s is
+      // multiplied, and no further -- reading the whole stage ahead would
+      // need more registers than the accumulators leave.
+      half8_t af[2][FM];
+      half8_t bf[2][FN];
+      load_frags(0, af[0], bf[0]);
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) {
+        if (s + 1 < STEPS) load_frags(s + 1, af[(s + 1) & 1], bf[(s + 1) & 1]);
+        multiply(af[s & 1], bf[s & 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -242,10 +271,11 @@ struct MfmaTile {
   // columns 4j .. 4j+3, so C is read and D written as 16-byte vectors: a
   // dword access costs the address unit as much as a 16-byte one.
   //
-  // With 32-bit addressing all C vectors of the block are requested before
-  // any is used, through a buffer resource from (r0, c0) to the end of C:
-  // rows past M read as zero, so the loads need no branch and their latencies
-  // overlap.  Stores go through the same kind of resource; columns that cross
+  // With 32-bit addressing C is read through a buffer resource from (r0, c0)
+  // to the end of C: rows past M read as zero, so the loads need no branch.
+  // The block is written in chunks of EPI_ROWS 32-row groups, and all C
+  // vectors of the next chunk are requested before the current one is
+  // written, so their latencies overlap.  Stores go through the same kind of resource; columns that cross
   // N go element by element.
   template <bool WIDE>
   __device__ __forceinline__ static void store_tile(const gg_device_problem_desc& p, int r0, int c0, int lane,
@@ -255,56 +285,70 @@ struct MfmaTile {
     const int lrow = 4 * (lane >> 5) + q;  // row within an 8-row group
     const int lcol = (lane & 31) & ~3;     // first column of the lane's vector
     if constexpr (!WIDE) {
-      floatx4_t cv[FM][FN][4];
-      if (use_c) {
-        const __amdgpu_buffer_rsrc_t crs =
-            buffer_rsrc(p.c + ((int64_t)r0 * p.ldc + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldc + (p.n - c0)));
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const uint32_t off = 4u * ((uint32_t)(fm * 32 + 8 * g + lrow) * (uint32_t)p.ldc + fn * 32 + lcol);
-              cv[fm][fn][g] = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(crs, (int)off, 0, 0));
-            }
-      } else {
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) cv[fm][fn][g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      }
       const __amdgpu_buffer_rsrc_t drs =
           buffer_rsrc(p.d + ((int64_t)r0 * p.ldd + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldd + (p.n - c0)));
+      // C vectors of EPI_ROWS 32-row groups per chunk; the next chunk's C is
+      // requested before the current chunk is stored.
+      floatx4_t cv[2][EPI_ROWS][FN][4];
+      auto load_c = [&](int chunk, floatx4_t (&dst)[EPI_ROWS][FN][4]) {
+        if (use_c) {
+          const __amdgpu_buffer_rsrc_t crs =
+              buffer_rsrc(p.c + ((int64_t)r0 * p.ldc + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldc + (p.n - c0)));
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
+          for (int i = 0; i < EPI_ROWS; ++i)
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-          const int ncol = p.n - (c0 + fn * 32 + lcol);  // columns of the vector inside the matrix
+            for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                          acc[fm][fn][4 * g + 3]};
-            quad_transpose(v, q);
-            const int rrow = fm * 32 + 8 * g + lrow;
-            floatx4_t out;
+              for (int g = 0; g < 4; ++g) {
+                const int fm = chunk * EPI_ROWS + i;
+                const uint32_t off = 4u * ((uint32_t)(fm * 32 + 8 * g + lrow) * (uint32_t)p.ldc + fn * 32 + lcol);
+                dst[i][fn][g] = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(crs, (int)off, 0, 0));
+              }
+        } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[fm][fn][g][e], p.alpha, p.beta);
-            if (r0 + rrow >= p.m || ncol <= 0) continue;
-            const uint32_t off = 4u * ((uint32_t)rrow * (uint32_t)p.ldd + fn * 32 + lcol);
-            if (ncol >= 4) {
-              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) int, out),
-                                                     drs, (int)off, 0, 0);
-            } else {
+          for (int i = 0; i < EPI_ROWS; ++i)
 #pragma unroll
-              for (int e = 0; e < 3; ++e) {
-                if (e < ncol) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(out[e]), drs, (int)(off + 4 * e), 0, 0);
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) dst[i][fn][g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      };
+      load_c(0, cv[0]);
+#pragma unroll
+      for (int chunk = 0; chunk < FM / EPI_ROWS; ++chunk) {
+        if (chunk + 1 < FM / EPI_ROWS) load_c(chunk + 1, cv[(chunk + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < EPI_ROWS; ++i) {
+          const int fm = chunk * EPI_ROWS + i;
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            const int ncol = p.n - (c0 + fn * 32 + lcol);  // columns of the vector inside the matrix
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float v[4] = {acc[fm][fn][4 * g + 0], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                            acc[fm][fn][4 * g + 3]};
+              quad_transpose(v, q);
+              const int rrow = fm * 32 + 8 * g + lrow;
+              floatx4_t out;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[chunk & 1][i][fn][g][e], p.alpha, p.beta);
+              if (r0 + rrow >= p.m || ncol <= 0) continue;
+              const uint32_t off = 4u * ((uint32_t)rrow * (uint32_t)p.ldd + fn * 32 + lcol);
+              if (ncol >= 4) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) int, out), drs, (int)off, 0, 0);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 3; ++e) {
+                  if (e < ncol) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(out[e]), drs, (int)(off + 4 * e), 0, 0);
+                }
               }
             }
           }
         }
+        // Keep each chunk's loads and stores in place: hoisting every C load
+        // to the top would hold the whole block's C in registers.
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
 #pragma unroll
@@ -428,8 +472,9 @@ struct FmaTile {
   }
 };
 
-template <int PATH, class G> struct TileFor;
-template <class G> struct TileFor<GGK_PATH_MFMA, G> { using type = MfmaTile<G>; };
-template <class G> struct TileFor<GGK_PATH_FMA, G> { using type = FmaTile<G>; };
+// The tile code of kernel shape S (gg_common.h).
+template <class S, int PATH> struct TileFor;
+template <class S> struct TileFor<S, GGK_PATH_MFMA> { using type = MfmaTile<typename S::G, S::WAVE_M>; };
+template <class S> struct TileFor<S, GGK_PATH_FMA> { using type = FmaTile<typename S::G>; };
 
 }  // namespace gg

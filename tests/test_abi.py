@@ -58,7 +58,8 @@ def test_cpp_api_header_mirrors_reference_names():
 
 def test_addressing_form_classifier():
     """ggk_needs_addr64 (host-only) picks 64-bit addressing exactly when a problem's tile offsets would
-    not fit 32 bits: work-tile rows * lda >= 2^30 or 64 * ldb >= 2^30, or a negative leading dimension."""
+    not stay below 2^31 bytes: work-tile rows * lda + K + 8 * stage_k >= 2^30 or stage_k * ldb >= 2^30
+    (elements), or a negative leading dimension."""
     lib = _lib.lib()
     shape = _lib.GGKWorkShape()
 
@@ -72,7 +73,8 @@ def test_addressing_form_classifier():
         for path in (_lib.GGK_PATH_FMA, _lib.GGK_PATH_MFMA):
             assert lib.ggk_work_shape_get(variant, path, shape) == 0
             assert shape.rows == cta_m * shape.tiles_m and shape.stage_k in (32, 64)
-            limit_a = (1 << 30) // shape.rows
+            # smallest lda that does not fit, for K = 1
+            limit_a = ((1 << 30) - 2 - 8 * shape.stage_k) // shape.rows + 1
             limit_b = (1 << 30) // shape.stage_k
             assert needs(variant, path, limit_a - 1, 8) == 0
             assert needs(variant, path, limit_a, 8) == 1
@@ -89,4 +91,4 @@ def test_addressing_form_classifier():
             assert needs(variant, path, 8, 8, ldc=(1 << 27) - 1, c=64, beta=0.5) == 0
     assert lib.ggk_needs_addr64(7, 0, _lib.GGDeviceProblemDesc()) == -1
     assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_128x64x32, _lib.GGK_PATH_MFMA, shape) == 0
-    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 2, 512, 256, 64)
+    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 4, 512, 256, 64)

@@ -139,43 +139,74 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
   return hipSuccess;
 }
 
-// Splits the work-tile indices [0, total) into GGK_SCHEDULER_CHUNKS contiguous
-// chunks of about equal memory cost, one per XCD.  A work tile of problem p
-// moves up to (BM + BN) * k binary16 values in and BM * BN floats out (twice
-// when C is read); the grouped kernel on these shapes is bound by those bytes.
-std::array<int, GGK_SCHEDULER_CHUNKS + 1> plan_chunks(const std::vector<DeviceProblemDesc>& problems,
-                                                      const std::vector<int>& offsets, int bm, int bn) {
+// The order in which the grouped kernel meets the problems' work tiles, and
+// its split into GGK_SCHEDULER_CHUNKS contiguous chunks, one per XCD.
+struct Schedule {
+  std::vector<int> order;         // problem (sorted index) at each position
+  std::vector<int> work_offsets;  // prefix sums of the work-tile counts in that order
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> bounds{};
+};
+
+// Estimated time of one work tile of problem p, in cycles of one CU: a fixed
+// part (finding the tile, the first stage's latency, the barriers around the
+// claim), a k-loop whose stages move (rows + cols) x 64 binary16 values each,
+// and an epilogue that moves rows x cols floats (twice when C is read).  The
+// constants come from per-phase clock stamps of the grouped kernel; only the
+// ratios between problems matter.
+double work_tile_time(const DeviceProblemDesc& p, int bm, int bn, int bk) {
+  if (p.m <= 0 || p.n <= 0) return 0.0;
+  const double rows = static_cast<double>(p.m) / ceil_div(p.m, bm);  // mean rows of the problem's tiles
+  const double cols = static_cast<double>(p.n) / ceil_div(p.n, bn);
+  const double stages = ceil_div(std::max(p.k, 0), bk);
+  const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+  return 8000.0 + stages * (400.0 + 4.0 * (rows + cols)) + 0.2 * rows * cols * (reads_c ? 2.0 : 1.0);
+}
+
+// Longest processing time first at two levels.  Problems go whole to the XCD
+// chunk with the least estimated work so far, largest problems first (a
+// problem's tiles share A and B panels, which that XCD's L2 then serves);
+// within a chunk the tiles with the longest estimated time come first, so
+// the last tiles any workgroup starts are short ones.  Every order yields the
+// same D: each work tile is computed the same way wherever it runs.
+Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std::vector<int>& work, int bm, int bn,
+                       int bk) {
   constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
-  std::array<int, kChunks + 1> bounds{};
-  const int total = offsets.back();
-  std::vector<double> cost(problems.size());
-  double sum = 0.0;
-  for (size_t i = 0; i < problems.size(); ++i) {
-    const DeviceProblemDesc& p = problems[i];
-    const bool reads_c = p.c != nullptr && p.beta != 0.0f;
-    const double rows = std::min(bm, std::max(p.m, 0));
-    const double cols = std::min(bn, std::max(p.n, 0));
-    cost[i] = 2.0 * (rows + cols) * std::max(p.k, 0) + 4.0 * rows * cols * (reads_c ? 2.0 : 1.0);
-    sum += cost[i] * (offsets[i + 1] - offsets[i]);
+  const int count = static_cast<int>(problems.size());
+  std::vector<double> tile_time(count), total(count);
+  for (int i = 0; i < count; ++i) {
+    tile_time[i] = work[i] > 0 ? work_tile_time(problems[i], bm, bn, bk) : 0.0;
+    total[i] = tile_time[i] * work[i];
   }
-  bounds[0] = 0;
-  bounds[kChunks] = total;
-  double before = 0.0;  // cost of all work tiles of problems before i
-  size_t i = 0;
-  for (int c = 1; c < kChunks; ++c) {
-    const double target = sum * c / kChunks;
-    while (i < problems.size() && before + cost[i] * (offsets[i + 1] - offsets[i]) < target) {
-      before += cost[i] * (offsets[i + 1] - offsets[i]);
-      ++i;
+  std::vector<int> by_total(count);
+  for (int i = 0; i < count; ++i) by_total[i] = i;
+  std::stable_sort(by_total.begin(), by_total.end(), [&](int x, int y) { return total[x] > total[y]; });
+  std::array<double, kChunks> load{};
+  std::array<std::vector<int>, kChunks> members;
+  for (const int i : by_total) {
+    int c = 0;
+    for (int d = 1; d < kChunks; ++d) {
+      if (load[d] < load[c]) c = d;
     }
-    int t = total;
-    if (i < problems.size()) {
-      const int into = cost[i] > 0.0 ? static_cast<int>((target - before) / cost[i]) : 0;
-      t = std::min(offsets[i] + into, offsets[i + 1]);
-    }
-    bounds[c] = std::max(bounds[c - 1], std::min(t, total));
+    load[c] += total[i];
+    members[c].push_back(i);
   }
-  return bounds;
+  Schedule s;
+  s.order.reserve(count);
+  s.work_offsets.assign(1, 0);
+  s.work_offsets.reserve(count + 1);
+  s.bounds[0] = 0;
+  for (int c = 0; c < kChunks; ++c) {
+    std::vector<int>& m = members[c];
+    std::stable_sort(m.begin(), m.end(), [&](int x, int y) {
+      return tile_time[x] != tile_time[y] ? tile_time[x] > tile_time[y] : x < y;
+    });
+    for (const int i : m) {
+      s.order.push_back(i);
+      s.work_offsets.push_back(s.work_offsets.back() + work[i]);
+    }
+    s.bounds[c + 1] = s.work_offsets.back();
+  }
+  return s;
 }
 
 void release(DeviceProblemDesc*& problems, int*& offsets, int*& state) {
@@ -302,7 +333,8 @@ hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info) {
 struct GroupedGemmExecutor::Impl {
   DeviceProblemDesc* d_problems = nullptr;
   int* d_tile_offsets = nullptr;  // [problem_count + 1] reference tile offsets, then
-                                  // [problem_count + 1] work-tile offsets
+                                  // [problem_count + 1] work-tile offsets in scheduling
+                                  // order, then [problem_count] the scheduling order
   int* d_state = nullptr;
 
   int problem_count = 0;
@@ -369,10 +401,7 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
 
   std::vector<DeviceProblemDesc> device_problems;
   device_problems.reserve(problem_count);
-  // Reference tile offsets followed by the work-tile offsets of the same order.
-  std::vector<int> offsets(prepared.tile_offsets);
-  offsets.reserve(2 * (problem_count + 1));
-  offsets.push_back(0);
+  std::vector<int> work(problem_count);
   if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
   for (int i = 0; i < problem_count; ++i) {
     const ProblemDesc& p = prepared.sorted_problems[i];
@@ -383,14 +412,20 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
       return hipErrorInvalidValue;
     }
-    const int64_t work = static_cast<int64_t>(ceil_div(dp.tiles_m, mode.work.tiles_m)) *
-                         ceil_div(dp.tiles_n, mode.work.tiles_n);
-    offsets.push_back(static_cast<int>(offsets.back() + work));  // never above the tile count
+    // Never above the problem's tile count, so the sums fit an int.
+    work[i] = ceil_div(dp.tiles_m, mode.work.tiles_m) * ceil_div(dp.tiles_n, mode.work.tiles_n);
     if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
     device_problems.push_back(dp);
   }
-  const std::vector<int> work_offsets(offsets.begin() + problem_count + 1, offsets.end());
-  impl_->total_work = work_offsets.back();
+  const Schedule schedule = plan_schedule(device_problems, work, config.cta_m * mode.work.tiles_m,
+                                          config.cta_n * mode.work.tiles_n, mode.work.stage_k);
+  impl_->total_work = schedule.work_offsets.back();
+  impl_->chunk_bounds = schedule.bounds;
+  // Device ints: the reference tile offsets (sorted order), the work-tile
+  // offsets (scheduling order), the scheduling order.
+  std::vector<int> offsets(prepared.tile_offsets);
+  offsets.insert(offsets.end(), schedule.work_offsets.begin(), schedule.work_offsets.end());
+  offsets.insert(offsets.end(), schedule.order.begin(), schedule.order.end());
 
   if (problem_count > 0) {
     status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems),
@@ -411,8 +446,6 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (status != hipSuccess) return status;
   }
 
-  impl_->chunk_bounds = plan_chunks(device_problems, work_offsets, config.cta_m * mode.work.tiles_m,
-                                    config.cta_n * mode.work.tiles_n);
 
   OccupancyInfo occupancy{};
   status = fill_occupancy(config, mode, &occupancy);
@@ -429,7 +462,8 @@ hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                            impl_->d_tile_offsets + impl_->problem_count + 1, impl_->problem_count,
+                            impl_->d_tile_offsets + impl_->problem_count + 1,
+                            impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->problem_count,
                             impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(), impl_->grid_ctas,
                             stream);
 }
@@ -438,8 +472,8 @@ hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_cloc
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                                   impl_->d_tile_offsets,
-                                   impl_->d_tile_offsets + impl_->problem_count + 1, impl_->problem_count,
+                                   impl_->d_tile_offsets, impl_->d_tile_offsets + impl_->problem_count + 1,
+                                   impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->problem_count,
                                    impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(),
                                    impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
 }

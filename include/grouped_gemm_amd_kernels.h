@@ -146,8 +146,8 @@ hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out);
 
 /* Addressing form of a grouped launch.  GGK_ADDR_32: A and B are addressed
  * and C/D with 32-bit offsets from per-tile origins, which needs, for every
- * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda < 2^30, stage_k * ldb
- * < 2^30 (ggk_work_shape), 0 <= ldd < 2^27 and, when C is read (c != NULL and
+ * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda + k + 8 * stage_k <
+ * 2^30, stage_k * ldb < 2^30 (ggk_work_shape), 0 <= ldd < 2^27 and, when C is read (c != NULL and
  * beta != 0), 0 <= ldc < 2^27.  GGK_ADDR_64: 64-bit addresses, any layout, slower.
  * ggk_needs_addr64 returns 1 when `problem` (host memory) needs GGK_ADDR_64,
  * 0 when not (also for a problem without tiles), -1 for a bad argument.  The
@@ -157,28 +157,32 @@ int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* proble
 
 /* Persistent grouped launch (launch_grouped_by_variant + grouped_gemm_kernel,
  * src/grouped_gemm.cu:640-675, 728-751, 800-869).  d_problems[problem_count]
- * in sorted order; d_work_offsets[problem_count + 1] is the prefix sum of the
- * problems' work-tile counts (the role of the reference's d_tile_offsets,
- * which it equals when the work tile is one macro-tile); d_state holds
+ * in sorted order.  Work tiles are numbered in a scheduling order of the
+ * problems: d_order[problem_count] (device memory, or NULL for the sorted
+ * order itself) gives the problem at each position, and
+ * d_work_offsets[problem_count + 1] is the prefix sum of the work-tile counts
+ * in that order (the role of the reference's d_tile_offsets, which it equals
+ * when the work tile is one macro-tile and d_order is NULL); d_state holds
  * GGK_SCHEDULER_STATE_INTS zeroed ints.  chunk_bounds (host memory,
  * GGK_SCHEDULER_CHUNKS + 1 non-decreasing ints from 0 to total_work, or NULL
  * for equal counts) splits the work-tile indices into the per-XCD chunks.
  * grid workgroups claim work tiles until total_work are done. */
 hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
-                              const int* d_work_offsets, int problem_count, int total_work, int* d_state,
-                              const int* chunk_bounds, int grid, hipStream_t stream);
+                              const int* d_work_offsets, const int* d_order, int problem_count, int total_work,
+                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream);
 
 /* The same scheduler with instrumentation.  d_tile_map (may be NULL; needs
- * d_tile_offsets, the reference tile offsets): for each reference tile t of a
- * claimed work tile, ints [3t, 3t+3) receive (problem, tile_m, tile_n) and no
+ * d_tile_offsets, the reference tile offsets of the problems in sorted
+ * order): for each reference tile t of a claimed work tile, ints [3t, 3t+3)
+ * receive (problem, tile_m, tile_n), problem in sorted order, and no
  * GEMM is computed.  d_wg_clock (may be NULL): for workgroup w, the 100 MHz
  * wall clock at its start and at the end of its last tile go to [2w, 2w+2);
  * the GEMM is computed as usual. */
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
-                                     const int* d_work_offsets, int problem_count, int total_work, int* d_state,
-                                     const int* chunk_bounds, int grid, int* d_tile_map, long long* d_wg_clock,
-                                     hipStream_t stream);
+                                     const int* d_work_offsets, const int* d_order, int problem_count,
+                                     int total_work, int* d_state, const int* chunk_bounds, int grid,
+                                     int* d_tile_map, long long* d_wg_clock, hipStream_t stream);
 
 /* Device-resident preparation of a mixture-of-experts group (no reference
  * counterpart: it is the step before the grouped launch in MoE use, done here

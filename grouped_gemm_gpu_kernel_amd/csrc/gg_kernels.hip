@@ -394,6 +394,7 @@ struct KernelEntry {
   static constexpr int tm = KernelShape<V, P>::TM;
   static constexpr int tn = KernelShape<V, P>::TN;
   static constexpr int bm = KernelShape<V, P>::G::BM;
+  static constexpr int bn = KernelShape<V, P>::G::BN;
   static constexpr int bk = KernelShape<V, P>::G::BK;
 };
 
@@ -401,7 +402,8 @@ struct KernelEntry {
   {{gg_grouped_kernel<V, P, false, false>, gg_grouped_kernel<V, P, false, true>},                   \
    {gg_grouped_kernel<V, P, true, false>, gg_grouped_kernel<V, P, true, true>},                     \
    {gg_single_kernel<V, P, false>, gg_single_kernel<V, P, true>}, KernelEntry<V, P>::threads,        \
-   KernelEntry<V, P>::tm, KernelEntry<V, P>::tn, KernelEntry<V, P>::bm, KernelEntry<V, P>::bk}
+   KernelEntry<V, P>::tm, KernelEntry<V, P>::tn, KernelEntry<V, P>::bm, KernelEntry<V, P>::bn,      \
+   KernelEntry<V, P>::bk}
 #define GG_ROW(V) {GG_ENTRY(V, 0), GG_ENTRY(V, 1)}
 
 struct KernelSet {
@@ -412,6 +414,7 @@ struct KernelSet {
   int tm;
   int tn;
   int bm;  // work-tile rows
+  int bn;  // work-tile columns
   int bk;  // stage depth
 };
 
@@ -537,17 +540,17 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
 
 // 32-bit offsets from a work tile's origin reach every A and B value the
 // tile reads when 0 <= lda, 0 <= ldb, BM * lda + K + 8 BK < 2^30 and
-// BK * ldb < 2^30 (elements; the loader also requests a few stages past K);
-// the epilogue's per-lane offsets (a few rows of C or D) when 0 <= ldc, ldd
-// < 2^27 (ldc only matters when C is read).  Every byte offset then stays
-// below 2^31, which the loader's out-of-range marker relies on.
+// BK * ldb < 2^30 (binary16 elements; the bound leaves room past K), and
+// every C and D value of the tile when 0 <= ldc, ldd and BM * ld + BN < 2^29
+// (float elements; ldc only matters when C is read).  Every byte offset then
+// stays below 2^31, which the loader's out-of-range marker relies on.
 static bool fits_addr32(const KernelSet& k, const gg_device_problem_desc& p) {
   constexpr int64_t kLimit = int64_t(1) << 30;
-  constexpr int64_t kLdLimit = int64_t(1) << 27;
+  constexpr int64_t kOutLimit = int64_t(1) << 29;
   const bool reads_c = p.c != nullptr && p.beta != 0.0f;
   return p.lda >= 0 && p.ldb >= 0 && p.k >= 0 && (int64_t)k.bm * p.lda + p.k + 8 * k.bk < kLimit &&
-         (int64_t)k.bk * p.ldb < kLimit && p.ldd >= 0 && p.ldd < kLdLimit &&
-         (!reads_c || (p.ldc >= 0 && p.ldc < kLdLimit));
+         (int64_t)k.bk * p.ldb < kLimit && p.ldd >= 0 && (int64_t)k.bm * p.ldd + k.bn < kOutLimit &&
+         (!reads_c || (p.ldc >= 0 && (int64_t)k.bm * p.ldc + k.bn < kOutLimit));
 }
 
 hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out) {

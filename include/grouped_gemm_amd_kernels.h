@@ -147,8 +147,10 @@ hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out);
 /* Addressing form of a grouped launch.  GGK_ADDR_32: A and B are addressed
  * and C/D with 32-bit offsets from per-tile origins, which needs, for every
  * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda + k + 8 * stage_k <
- * 2^30, stage_k * ldb < 2^30 (ggk_work_shape), 0 <= ldd < 2^27 and, when C is read (c != NULL and
- * beta != 0), 0 <= ldc < 2^27.  GGK_ADDR_64: 64-bit addresses, any layout, slower.
+ * 2^30, stage_k * ldb < 2^30 (ggk_work_shape), 0 <= ldd, rows * ldd + cols <
+ * 2^29 (cols = tiles_n x the configuration's macro-tile width) and, when C is
+ * read (c != NULL and beta != 0), the same for ldc.  GGK_ADDR_64: 64-bit
+ * addresses, any layout, slower.
  * ggk_needs_addr64 returns 1 when `problem` (host memory) needs GGK_ADDR_64,
  * 0 when not (also for a problem without tiles), -1 for a bad argument.  The
  * single-problem launch chooses by itself.  No reference counterpart. */

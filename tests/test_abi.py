@@ -59,7 +59,8 @@ def test_cpp_api_header_mirrors_reference_names():
 def test_addressing_form_classifier():
     """ggk_needs_addr64 (host-only) picks 64-bit addressing exactly when a problem's tile offsets would
     not stay below 2^31 bytes: work-tile rows * lda + K + 8 * stage_k >= 2^30 or stage_k * ldb >= 2^30
-    (elements), or a negative leading dimension."""
+    (binary16 elements), rows * ldd + cols >= 2^29 or, when C is read, rows * ldc + cols >= 2^29 (float
+    elements), or a negative leading dimension."""
     lib = _lib.lib()
     shape = _lib.GGKWorkShape()
 
@@ -68,8 +69,8 @@ def test_addressing_form_classifier():
                                      tiles_m=tiles, tiles_n=tiles)
         return lib.ggk_needs_addr64(variant, path, p)
 
-    for variant, cta_m in ((_lib.GGK_VARIANT_64x64x16, 64), (_lib.GGK_VARIANT_128x64x32, 128),
-                           (_lib.GGK_VARIANT_64x128x32, 64)):
+    for variant, cta_m, cta_n in ((_lib.GGK_VARIANT_64x64x16, 64, 64), (_lib.GGK_VARIANT_128x64x32, 128, 64),
+                                  (_lib.GGK_VARIANT_64x128x32, 64, 128)):
         for path in (_lib.GGK_PATH_FMA, _lib.GGK_PATH_MFMA):
             assert lib.ggk_work_shape_get(variant, path, shape) == 0
             assert shape.rows == cta_m * shape.tiles_m and shape.stage_k in (32, 64)
@@ -82,13 +83,15 @@ def test_addressing_form_classifier():
             assert needs(variant, path, 8, limit_b) == 1
             assert needs(variant, path, -1, 8) == 1 and needs(variant, path, 8, -1) == 1
             assert needs(variant, path, 1 << 30, 1 << 30, tiles=0) == 0  # no tiles, nothing addressed
-            assert needs(variant, path, 8, 8, ldd=(1 << 27) - 1) == 0
-            assert needs(variant, path, 8, 8, ldd=1 << 27) == 1
+            # smallest ldc / ldd that does not fit
+            limit_out = ((1 << 29) - 1 - cta_n * shape.tiles_n) // shape.rows + 1
+            assert needs(variant, path, 8, 8, ldd=limit_out - 1) == 0
+            assert needs(variant, path, 8, 8, ldd=limit_out) == 1
             # ldc matters only when C is read
-            assert needs(variant, path, 8, 8, ldc=1 << 27) == 0
-            assert needs(variant, path, 8, 8, ldc=1 << 27, c=64, beta=0.0) == 0
-            assert needs(variant, path, 8, 8, ldc=1 << 27, c=64, beta=0.5) == 1
-            assert needs(variant, path, 8, 8, ldc=(1 << 27) - 1, c=64, beta=0.5) == 0
+            assert needs(variant, path, 8, 8, ldc=limit_out) == 0
+            assert needs(variant, path, 8, 8, ldc=limit_out, c=64, beta=0.0) == 0
+            assert needs(variant, path, 8, 8, ldc=limit_out, c=64, beta=0.5) == 1
+            assert needs(variant, path, 8, 8, ldc=limit_out - 1, c=64, beta=0.5) == 0
     assert lib.ggk_needs_addr64(7, 0, _lib.GGDeviceProblemDesc()) == -1
     assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_128x64x32, _lib.GGK_PATH_MFMA, shape) == 0
     assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 4, 512, 256, 64)

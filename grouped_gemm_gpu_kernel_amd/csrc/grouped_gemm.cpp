@@ -148,18 +148,19 @@ struct Schedule {
 };
 
 // Estimated time of one work tile of problem p, in cycles of one CU: a fixed
-// part (finding the tile, the first stage's latency, the barriers around the
-// claim), a k-loop whose stages move (rows + cols) x 64 binary16 values each,
-// and an epilogue that moves rows x cols floats (twice when C is read).  The
-// constants come from per-phase clock stamps of the grouped kernel; only the
-// ratios between problems matter.
+// part (finding the tile, the first stage's latency, the claim), a k-loop
+// whose stages cost mostly their latency plus a little per row and column
+// they move, and an epilogue that moves rows x cols floats (twice when C is
+// read).  The constants are a least-squares fit to per-tile clock stamps of
+// the grouped kernel on mixed shapes (median error 7%); only the ratios
+// between problems matter.
 double work_tile_time(const DeviceProblemDesc& p, int bm, int bn, int bk) {
   if (p.m <= 0 || p.n <= 0) return 0.0;
   const double rows = static_cast<double>(p.m) / ceil_div(p.m, bm);  // mean rows of the problem's tiles
   const double cols = static_cast<double>(p.n) / ceil_div(p.n, bn);
   const double stages = ceil_div(std::max(p.k, 0), bk);
   const bool reads_c = p.c != nullptr && p.beta != 0.0f;
-  return 8000.0 + stages * (400.0 + 4.0 * (rows + cols)) + 0.2 * rows * cols * (reads_c ? 2.0 : 1.0);
+  return 15000.0 + stages * (3100.0 + 2.9 * (rows + cols)) + 0.23 * rows * cols * (reads_c ? 2.0 : 1.0);
 }
 
 // Longest processing time first at two levels.  Problems go whole to the XCD

@@ -131,6 +131,12 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
 // addresses row kb + j/4, columns nb + 4*(j%4), and lane i receives
 // B[kb + e][nb + i].
 // ---------------------------------------------------------------------------
+// Epilogue chunks of C requested ahead of the one being written (for blocks
+// written in three or more chunks): C comes from HBM, and with two chunks in
+// flight its latency is paid about half as often.
+#ifndef GG_EPI_AHEAD
+#define GG_EPI_AHEAD 2
+#endif
 template <class G, int WM_>
 struct MfmaTile {
   static constexpr int WM = WM_;
@@ -274,8 +280,8 @@ struct MfmaTile {
   // With 32-bit addressing C is read through a buffer resource from (r0, c0)
   // to the end of C: rows past M read as zero, so the loads need no branch.
   // The block is written in chunks of EPI_ROWS 32-row groups, and all C
-  // vectors of the next chunk are requested before the current one is
-  // written, so their latencies overlap.  Stores go through the same kind of resource; columns that cross
+  // vectors of the next chunk (two, for blocks of three or more chunks) are
+  // requested before the current one is written, so their latencies overlap.  Stores go through the same kind of resource; columns that cross
   // N go element by element.
   template <bool WIDE>
   __device__ __forceinline__ static void store_tile(const gg_device_problem_desc& p, int r0, int c0, int lane,
@@ -287,9 +293,11 @@ struct MfmaTile {
     if constexpr (!WIDE) {
       const __amdgpu_buffer_rsrc_t drs =
           buffer_rsrc(p.d + ((int64_t)r0 * p.ldd + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldd + (p.n - c0)));
-      // C vectors of EPI_ROWS 32-row groups per chunk; the next chunk's C is
-      // requested before the current chunk is stored.
-      floatx4_t cv[2][EPI_ROWS][FN][4];
+      // C vectors of EPI_ROWS 32-row groups per chunk; the C of the next
+      // AHEAD chunks is requested before the current chunk is stored.
+      constexpr int CHUNKS = FM / EPI_ROWS;
+      constexpr int AHEAD = CHUNKS >= 3 ? GG_EPI_AHEAD : 1;  // chunks of C requested ahead
+      floatx4_t cv[AHEAD + 1][EPI_ROWS][FN][4];
       auto load_c = [&](int chunk, floatx4_t (&dst)[EPI_ROWS][FN][4]) {
         if (use_c) {
           const __amdgpu_buffer_rsrc_t crs =
@@ -313,10 +321,13 @@ struct MfmaTile {
               for (int g = 0; g < 4; ++g) dst[i][fn][g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
       };
-      load_c(0, cv[0]);
 #pragma unroll
-      for (int chunk = 0; chunk < FM / EPI_ROWS; ++chunk) {
-        if (chunk + 1 < FM / EPI_ROWS) load_c(chunk + 1, cv[(chunk + 1) & 1]);
+      for (int c = 0; c < AHEAD; ++c) {
+        if (c < CHUNKS) load_c(c, cv[c]);
+      }
+#pragma unroll
+      for (int chunk = 0; chunk < CHUNKS; ++chunk) {
+        if (chunk + AHEAD < CHUNKS) load_c(chunk + AHEAD, cv[(chunk + AHEAD) % (AHEAD + 1)]);
 #pragma unroll
         for (int i = 0; i < EPI_ROWS; ++i) {
           const int fm = chunk * EPI_ROWS + i;
@@ -331,7 +342,7 @@ struct MfmaTile {
               const int rrow = fm * 32 + 8 * g + lrow;
               floatx4_t out;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[chunk & 1][i][fn][g][e], p.alpha, p.beta);
+              for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[chunk % (AHEAD + 1)][i][fn][g][e], p.alpha, p.beta);
               if (r0 + rrow >= p.m || ncol <= 0) continue;
               const uint32_t off = 4u * ((uint32_t)rrow * (uint32_t)p.ldd + fn * 32 + lcol);
               if (ncol >= 4) {

@@ -562,6 +562,7 @@ struct DmaLoader {
   int b_row, b_col8;       // piece 0: k-row within the stage and global piece index
   int m0, n0;
   int last_stage;
+  bool a_fix, b_fix;  // whether the matrices' last values must be put back (see the constructor)
   uint32_t a_last, b_last;
 
   __device__ __forceinline__ DmaLoader(const gg_device_problem_desc& p, int m0_, int n0_)
@@ -589,8 +590,17 @@ struct DmaLoader {
     a_step = 2u * (uint32_t)A_ROWS_STEP * (uint32_t)p.lda;
     b_step = 2u * (uint32_t)B_ROWS_STEP * (uint32_t)p.ldb;
     last_stage = (p.k - 1) / G::BK;
-    a_last = p.k > 0 ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
-    b_last = p.k > 0 ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
+    // A matrix's last value reads as zero only where the dword that holds it
+    // would reach 2 bytes past the matrix, i.e. where it sits at an even
+    // element of its 16-byte piece.  Pieces start at k = 8c for A and at
+    // column n0 + 8c (n0 even) for B, so that happens for A exactly when K is
+    // odd and for B when N is odd, and only in the tile holding A's last row
+    // or B's last column: only then is the value read (a scalar load from
+    // memory, which a barrier's wait would otherwise sit out for every tile).
+    a_fix = (p.k & 1) != 0 && m0 + G::BM >= p.m;
+    b_fix = (p.n & 1) != 0 && n0 + G::BN >= p.n;
+    a_last = a_fix ? load_value_uniform(A + (int64_t)(p.m - 1) * p.lda + (p.k - 1)) : 0u;
+    b_last = b_fix ? load_value_uniform(B + (int64_t)(p.k - 1) * p.ldb + (p.n - 1)) : 0u;
   }
 
   // Byte offset no load reaches: the 32-bit addressing form keeps every
@@ -634,7 +644,7 @@ struct DmaLoader {
       const int col = kt * G::BK + 8 * a_col8;
       const int row = m0 + a_row + i * A_ROWS_STEP;
       u32x4_t val = keep_values(*slot, k - col);
-      val = put_value(val, row == m - 1 ? k - 1 - col : -1, a_last);
+      val = put_value(val, a_fix && row == m - 1 ? k - 1 - col : -1, a_last);
       *slot = val;
     }
 #pragma unroll
@@ -644,7 +654,7 @@ struct DmaLoader {
       const int col = n0 + 8 * b_col8;
       const u32x4_t zero = {0u, 0u, 0u, 0u};
       u32x4_t val = krow < k ? *slot : zero;
-      val = put_value(val, krow == k - 1 ? n - 1 - col : -1, b_last);
+      val = put_value(val, b_fix && krow == k - 1 ? n - 1 - col : -1, b_last);
       *slot = val;
     }
   }

@@ -318,6 +318,42 @@ def test_padded_leading_dimensions(torch):
                 assert np.isnan(got[:, n:]).all(), "padding columns of D were written"
 
 
+def test_matrix_end_values(torch):
+    """The last value of A and of B (the dword that holds it can reach 2 bytes past the matrix and then
+    reads as zero; the loader puts the value back exactly where that happens: odd K for A, odd N for B)
+    -- every parity of K and N, matrices starting at even and odd element offsets, tight leading
+    dimensions, the last row and column in the first or a later work tile.  Both last values are 8
+    and all others at most 1/8 in magnitude, so a lost or overwritten last value is far outside the
+    bound."""
+    rng = np.random.default_rng(21)
+    for mfma in PATHS:
+        for config in CONFIGS:
+            cfg = KernelConfig.named(config, use_tensor_cores=mfma)
+            for (m, n, k) in [(37, 45, 19), (37, 46, 20), (37, 45, 20), (37, 46, 19), (300, 301, 33), (260, 258, 64)]:
+                for off in (0, 1):
+                    say(f"matrix ends {config} mfma={mfma} {(m, n, k)} off={off}")
+                    a = O.f32_to_f16(rng.uniform(-0.125, 0.125, m * k + off).astype(np.float32))
+                    b = O.f32_to_f16(rng.uniform(-0.125, 0.125, k * n + off).astype(np.float32))
+                    a[off + m * k - 1] = O.f32_to_f16(np.array([8.0], np.float32))[0]
+                    b[off + k * n - 1] = O.f32_to_f16(np.array([8.0], np.float32))[0]
+                    c = rng.uniform(-1, 1, m * n).astype(np.float32)
+                    da = torch.from_numpy(a.view(np.int16)).cuda()
+                    db = torch.from_numpy(b.view(np.int16)).cuda()
+                    dc = torch.from_numpy(c).cuda()
+                    dd = torch.full((m * n,), float("nan"), device="cuda")
+                    p = ProblemDesc(m, n, k, da.data_ptr() + 2 * off, db.data_ptr() + 2 * off, dc.data_ptr(),
+                                    dd.data_ptr(), k, n, n, n, 1.0, 0.5)
+                    assert api.run_grouped_gemm_once([p], SortMode.kNone, cfg) == 0
+                    torch.cuda.synchronize()
+                    got = dd.cpu().numpy()
+                    want = O.gemm(m, n, k, a[off:], k, b[off:], n, c, n, 1.0, 0.5)
+                    tol = tolerance(k, 8.0, 8.0, 1.0, 1.0, 0.5)
+                    err = np.abs(got - want).max()
+                    assert err <= tol, f"{config} mfma={mfma} {(m, n, k)} off={off}: err {err}"
+                    # the corner element holds the product of the two last values (64)
+                    assert abs(got[-1] - want[-1]) <= tol
+
+
 def test_wide_leading_dimensions(torch):
     """Leading dimensions too large for 32-bit tile offsets (lda * 256 >= 2^30, ldb * 64 >= 2^30) select
     the 64-bit addressing kernels, in a grouped launch mixed with ordinary problems and per problem."""

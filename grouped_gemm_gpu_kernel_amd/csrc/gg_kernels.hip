@@ -419,7 +419,8 @@ struct KernelSet {
 };
 
 static const KernelSet kKernels[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {
-    GG_ROW(GGK_VARIANT_64x64x16), GG_ROW(GGK_VARIANT_128x64x32), GG_ROW(GGK_VARIANT_64x128x32)};
+    GG_ROW(GGK_VARIANT_64x64x16), GG_ROW(GGK_VARIANT_128x64x32), GG_ROW(GGK_VARIANT_64x128x32),
+    GG_ROW(GGK_VARIANT_128x64x32_SMALL), GG_ROW(GGK_VARIANT_64x128x32_SMALL)};
 #undef GG_ROW
 #undef GG_ENTRY
 

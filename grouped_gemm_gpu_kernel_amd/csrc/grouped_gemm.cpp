@@ -392,6 +392,29 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
 
   release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
   impl_->problem_count = problem_count;
+  // A launch with few work tiles is bound by the latency of each tile's
+  // stages rather than by bandwidth: with at most two work tiles per CU,
+  // 128x64x32 and 64x128x32 run on 128 x 128 work tiles instead (four or two
+  // times as many, two workgroups per CU).  The reference tile map is the
+  // same either way.
+  const int small_variant = mode.variant == GGK_VARIANT_128x64x32   ? GGK_VARIANT_128x64x32_SMALL
+                            : mode.variant == GGK_VARIANT_64x128x32 ? GGK_VARIANT_64x128x32_SMALL
+                                                                    : -1;
+  if (mode.path == GGK_PATH_MFMA && small_variant >= 0) {
+    int64_t work = 0;
+    for (int i = 0; i < problem_count; ++i) {
+      const ProblemDesc& p = prepared.sorted_problems[i];
+      if (p.m <= 0 || p.n <= 0) continue;
+      work += static_cast<int64_t>(ceil_div(ceil_div(p.m, config.cta_m), mode.work.tiles_m)) *
+              ceil_div(ceil_div(p.n, config.cta_n), mode.work.tiles_n);
+    }
+    if (work <= 2 * static_cast<int64_t>(mode.device.compute_units)) {
+      mode.variant = small_variant;
+      status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
+      if (status != hipSuccess) return status;
+    }
+  }
+
   impl_->total_tiles = prepared.total_tiles;
   impl_->total_work = 0;
   impl_->grid_ctas = 0;

@@ -45,12 +45,18 @@ typedef struct gg_device_problem_desc {
   int tiles_n;
 } gg_device_problem_desc;
 
-/* Macro-tile shapes (src/grouped_gemm.cu:47-52). */
+/* Macro-tile shapes (src/grouped_gemm.cu:47-52).  The _SMALL variants have no
+ * counterpart in the reference: the same macro-tiles on 128 x 128 work tiles
+ * (two workgroups per CU) instead of 256 x 256 (128x64x32) or 128 x 256
+ * (64x128x32), which the executor picks for launches with few work tiles (see
+ * GroupedGemmExecutor::build). */
 enum {
   GGK_VARIANT_64x64x16 = 0,
   GGK_VARIANT_128x64x32 = 1,
   GGK_VARIANT_64x128x32 = 2,
-  GGK_VARIANT_COUNT = 3
+  GGK_VARIANT_128x64x32_SMALL = 3,
+  GGK_VARIANT_64x128x32_SMALL = 4,
+  GGK_VARIANT_COUNT = 5
 };
 
 /* Tile compute path: FMA (the reference's SIMT path) or MFMA (the reference's

@@ -393,25 +393,27 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
   impl_->problem_count = problem_count;
   // A launch with few work tiles is bound by the latency of each tile's
-  // stages rather than by bandwidth: with at most two work tiles per CU,
-  // 128x64x32 and 64x128x32 run on 128 x 128 work tiles instead (four or two
-  // times as many, two workgroups per CU).  The reference tile map is the
-  // same either way.
+  // stages rather than by bandwidth: when the 128 x 128 work tiles of the
+  // small-set variants number at most two per workgroup slot (two
+  // workgroups per CU), 128x64x32 and 64x128x32 run on those instead of their
+  // 256 x 256 / 128 x 256 tiles.  The reference tile map is the same either way.
   const int small_variant = mode.variant == GGK_VARIANT_128x64x32   ? GGK_VARIANT_128x64x32_SMALL
                             : mode.variant == GGK_VARIANT_64x128x32 ? GGK_VARIANT_64x128x32_SMALL
                                                                     : -1;
   if (mode.path == GGK_PATH_MFMA && small_variant >= 0) {
+    ggk_work_shape small{};
+    status = ggk_work_shape_get(small_variant, mode.path, &small);
+    if (status != hipSuccess) return status;
     int64_t work = 0;
     for (int i = 0; i < problem_count; ++i) {
       const ProblemDesc& p = prepared.sorted_problems[i];
       if (p.m <= 0 || p.n <= 0) continue;
-      work += static_cast<int64_t>(ceil_div(ceil_div(p.m, config.cta_m), mode.work.tiles_m)) *
-              ceil_div(ceil_div(p.n, config.cta_n), mode.work.tiles_n);
+      work += static_cast<int64_t>(ceil_div(ceil_div(p.m, config.cta_m), small.tiles_m)) *
+              ceil_div(ceil_div(p.n, config.cta_n), small.tiles_n);
     }
-    if (work <= 2 * static_cast<int64_t>(mode.device.compute_units)) {
+    if (work <= 4 * static_cast<int64_t>(mode.device.compute_units)) {
       mode.variant = small_variant;
-      status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
-      if (status != hipSuccess) return status;
+      mode.work = small;
     }
   }
 

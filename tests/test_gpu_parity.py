@@ -419,6 +419,51 @@ def test_persistent_grid_sizes_and_repeated_runs(torch):
         ex.close()
 
 
+@pytest.mark.parametrize("config", ["128x64x32", "64x128x32"])
+def test_small_set_work_tiles_bit_identical(torch, config):
+    """A launch with few work tiles runs on the small-set variant (128 x 128 work tiles, two workgroups
+    per CU): 400 problems of 128 x 128 give a grid above one workgroup per CU, which only that variant
+    allows.  Its D is bit-identical to the per-problem baseline's, which runs the configuration's large
+    work tiles (every element goes through the same stages and MFMA steps), and matches the oracle on
+    sampled problems."""
+    say(f"small-set work tiles {config}")
+    count = 400
+    rng = np.random.default_rng(31)
+    m = np.full(count, 128, np.int64)
+    n = np.full(count, 128, np.int64)
+    k = rng.integers(33, 400, count)
+    spec = custom_spec("small400", m, n, k, alpha=rng.uniform(0.5, 2.0, count), beta=rng.uniform(0, 1, count),
+                       c_dist=("uniform", -1.0, 1.0), config=config)
+    dw = DeviceWorkload(spec)
+    probs = dw.problems()
+    cfg = KernelConfig.named(config)
+    ex = GroupedGemmExecutor()
+    assert ex.build(api.prepare_problem_set(probs, cfg, SortMode.kByK), cfg) == 0
+    assert ex.grid_ctas() > 256, "expected the small-set variant (two workgroups per CU)"
+    dw.poison_d()
+    assert ex.run() == 0
+    torch.cuda.synchronize()
+    grouped = dw.d.cpu().numpy().copy()
+    ex.close()
+    dw.poison_d()
+    assert api.run_baseline_per_problem(probs, cfg) == 0
+    torch.cuda.synchronize()
+    baseline = dw.d.cpu().numpy()
+    assert not np.isnan(grouped).any()
+    assert np.array_equal(grouped.view(np.uint32), baseline.view(np.uint32))
+    a = dw.a.cpu().numpy().view(np.uint16)
+    b = dw.b.cpu().numpy().view(np.uint16)
+    c = dw.c.cpu().numpy()
+    for i in (0, 137, count - 1):
+        p = probs[i]
+        ai = a[dw.a_off[i]:dw.a_off[i] + p.m * p.k]
+        bi = b[dw.b_off[i]:dw.b_off[i] + p.k * p.n]
+        ci = c[dw.c_off[i]:dw.c_off[i] + p.m * p.n]
+        want = O.gemm(p.m, p.n, p.k, ai, p.k, bi, p.n, ci, p.n, p.alpha, p.beta)
+        got = grouped[dw.d_off[i]:dw.d_off[i] + p.m * p.n]
+        assert np.abs(got - want).max() <= tolerance(p.k, 1.0, 1.0, 1.0, p.alpha, p.beta), i
+
+
 def test_wall_clock_trace(torch):
     spec = make_spec("plumbing16")
     dw = DeviceWorkload(spec)

@@ -140,7 +140,7 @@ SIGNATURES = {
     "gg_moe_create": (_i, [_P(GGKMoeLayout), _P(GGKernelConfig), _i, _P(_vp)]),
     "gg_moe_run": (_i, [_vp, _vp, _vp]),
     "gg_moe_grid_ctas": (_i, [_vp]),
-    "gg_moe_device_buffers": (_i, [_vp, _P(_vp), _P(_vp), _P(_vp), _P(_vp)]),
+    "gg_moe_device_buffers": (_i, [_vp, _P(_vp), _P(_vp), _P(_vp), _P(_vp), _P(_vp)]),
     "gg_moe_destroy": (None, [_vp]),
     # grouped_gemm_amd_kernels.h
     "ggk_alloc": (_i, [_P(_vp), ctypes.c_size_t]),
@@ -156,8 +156,8 @@ SIGNATURES = {
     "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
     "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp, _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
-    "ggk_moe_prepare": (_i, [_i, _i, _P(GGKMoeLayout), _vp, _i, _vp, _vp, _vp, _vp, _vp]),
-    "ggk_launch_grouped_device": (_i, [_i, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _vp]),
+    "ggk_moe_prepare": (_i, [_i, _i, _P(GGKMoeLayout), _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ggk_launch_grouped_device": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp]),
     "ggk_kernel_resources_get": (_i, [_i, _i, _i, _P(GGKKernelResources)]),
     "ggk_occupancy": (_i, [_i, _i, c_int_p]),
     "ggk_fill_uniform_f16": (_i, [_vp, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,

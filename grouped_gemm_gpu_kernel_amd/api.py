@@ -271,8 +271,8 @@ class MoeGroupedGemm:
         return _lib.lib().gg_moe_grid_ctas(self._handle)
 
     def device_buffers(self) -> tuple:
-        """(problems, offsets, sorted_to_original, header) device addresses."""
-        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        """(problems, offsets, sorted_to_original, header, order) device addresses."""
+        ptrs = [ctypes.c_void_p() for _ in range(5)]
         _lib.check(_lib.lib().gg_moe_device_buffers(self._handle, *[ctypes.byref(p) for p in ptrs]),
                    "gg_moe_device_buffers")
         return tuple(p.value or 0 for p in ptrs)

@@ -285,12 +285,13 @@ int gg_moe_run(const gg_moe* moe, const int* d_counts, hipStream_t stream) {
 int gg_moe_grid_ctas(const gg_moe* moe) { return moe != nullptr ? moe->moe.grid_ctas() : 0; }
 
 int gg_moe_device_buffers(const gg_moe* moe, const gg_device_problem_desc** problems, const int** offsets,
-                          const int** sorted_to_original, const int** header) {
+                          const int** sorted_to_original, const int** header, const int** order) {
   if (moe == nullptr) return hipErrorInvalidDevicePointer;
   if (problems != nullptr) *problems = moe->moe.device_problems();
   if (offsets != nullptr) *offsets = moe->moe.device_offsets();
   if (sorted_to_original != nullptr) *sorted_to_original = moe->moe.device_sorted_to_original();
   if (header != nullptr) *header = moe->moe.device_header();
+  if (order != nullptr) *order = moe->moe.device_order();
   return hipSuccess;
 }
 

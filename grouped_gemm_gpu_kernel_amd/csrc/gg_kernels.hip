@@ -579,8 +579,8 @@ hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_de
 }
 
 hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
-                                     const int* d_work_offsets, int problem_count, const int* d_header,
-                                     int* d_state, int grid, hipStream_t stream) {
+                                     const int* d_work_offsets, const int* d_order, int problem_count,
+                                     const int* d_header, int* d_state, int grid, hipStream_t stream) {
   if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 ||
       (addressing != GGK_ADDR_32 && addressing != GGK_ADDR_64)) {
     return hipErrorInvalidValue;
@@ -589,7 +589,7 @@ hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, cons
   if (d_problems == nullptr || d_work_offsets == nullptr || d_state == nullptr || d_header == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  GroupedArgs args{d_problems, nullptr, d_work_offsets, nullptr, problem_count, 0, d_state, nullptr, nullptr, {},
+  GroupedArgs args{d_problems, nullptr, d_work_offsets, d_order, problem_count, 0, d_state, nullptr, nullptr, {},
                    d_header};
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];

@@ -5,9 +5,10 @@
 // problem shapes on the host.  In MoE use the shapes are the per-expert token
 // counts, which a router produces on the GPU.  This kernel turns them into
 // the same prepared set -- descriptors in the sort mode's order, reference
-// tile offsets, work-tile offsets, the permutation, the per-XCD chunk bounds
-// -- in one workgroup, so the grouped launch can follow in stream order with
-// no host round trip.
+// tile offsets, the permutation, and the schedule the host build would plan:
+// the scheduling order, work-tile offsets in that order, the per-XCD chunk
+// bounds -- in one workgroup, so the grouped launch can follow in stream
+// order with no host round trip.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -30,11 +31,30 @@ struct MoeArgs {
   int sort_mode;
   int cta_m, cta_n;      // reference macro-tile
   int work_tm, work_tn;  // reference tiles per work tile
+  int stage_k;           // depth of one LDS stage
   gg_device_problem_desc* problems;
   int* offsets;
   int* perm;
+  int* order;
   int* header;
 };
+
+// Estimated time of all work tiles of one problem (tm x tn work tiles), in
+// hundredths of a cycle of one CU: per work tile 150 + stages * (31 + 0.029
+// (rows + cols)) + 0.0023 rows cols (twice that last term when C is read),
+// summed as integer products.  This is the host build's model
+// (problem_work_time in grouped_gemm.cpp), evaluated in the same order with
+// no fused multiply-add, so both give the same value and the same schedule.
+__device__ double problem_work_time(int m, int n, int k, int tm, int tn, int bk, bool reads_c) {
+#pragma clang fp contract(off)
+  if (m <= 0 || n <= 0 || tm <= 0 || tn <= 0) return 0.0;
+  const double w = static_cast<double>(tm) * tn;
+  const double stages = k > 0 ? (k - 1) / bk + 1 : 0;
+  const double edge = static_cast<double>(m) * tn + static_cast<double>(n) * tm;
+  const double stage = 310000.0 * w + 290.0 * edge;
+  const double area = static_cast<double>(m) * n;
+  return 1500000.0 * w + stages * stage + (reads_c ? 46.0 : 23.0) * area;
+}
 
 // Exclusive prefix sum of one value per thread over the workgroup, in thread
 // order; *total receives the sum.  Every thread must call it.
@@ -69,21 +89,24 @@ __device__ T block_exclusive_scan(T v, T* s_waves, T* total) {
 __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   __shared__ long long s_waves_ll[kWaves];
   __shared__ int s_waves_i[kWaves];
-  __shared__ double s_waves_d[kWaves];
   __shared__ int s_rows[kMaxExperts];
   __shared__ long long s_row0[kMaxExperts];
   __shared__ int s_tiles[kMaxExperts];
   __shared__ int s_perm[kMaxExperts];
-  __shared__ int s_work_off[kMaxExperts + 1];
-  __shared__ double s_cum[kMaxExperts];   // cost of the work tiles before sorted position i
-  __shared__ double s_cost[kMaxExperts];  // cost of one work tile of sorted position i
-  __shared__ int s_bounds[kChunks + 1];
+  __shared__ double s_total[kMaxExperts];    // estimated time of sorted position i
+  __shared__ double s_key[kMaxExperts];      // the same per work tile
+  __shared__ double s_by_total[kMaxExperts]; // estimated times, longest first
+  __shared__ int s_chunk[kMaxExperts];       // chunk of sorted position i
+  __shared__ int s_order[kMaxExperts];       // sorted position at each scheduling position
+  __shared__ int s_work[kMaxExperts];        // work tiles of sorted position i
+  __shared__ int s_chunk_work[kChunks];
   __shared__ int s_status;
 
   const ggk_moe_layout& L = args.layout;
   const int experts = L.experts;
   const int tid = threadIdx.x;
   if (tid == 0) s_status = 0;
+  if (tid < kChunks) s_chunk_work[tid] = 0;
   __syncthreads();
 
   // Rows of each expert: counts clamped to >= 0, origins by prefix sum, and
@@ -146,14 +169,11 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     work = tiles > 0 ? ((tiles_m + args.work_tm - 1) / args.work_tm) * ((tiles_n + args.work_tn - 1) / args.work_tn)
                      : 0;
   }
-  int total_tiles, total_work;
+  int total_tiles;
   const int tile_off = block_exclusive_scan<int>(tiles, s_waves_i, &total_tiles);
-  const int work_off = block_exclusive_scan<int>(work, s_waves_i, &total_work);
   const bool reads_c = L.c != nullptr && L.beta != 0.0f;
   if (pos < experts) {
     args.offsets[pos] = tile_off;
-    args.offsets[experts + 1 + pos] = work_off;
-    s_work_off[pos] = work_off;
     args.perm[pos] = ex;
     const long long r0 = s_row0[ex];
     gg_device_problem_desc p;
@@ -174,54 +194,98 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     p.tiles_n = tiles > 0 ? tiles_n : 0;
     args.problems[pos] = p;
   }
-  if (pos == 0) {
-    args.offsets[experts] = total_tiles;
-    args.offsets[2 * experts + 1] = total_work;
-    s_work_off[experts] = total_work;
-  }
+  if (pos == 0) args.offsets[experts] = total_tiles;
 
-  // Chunk bounds by memory cost, as the host plan does: a work tile moves up to
-  // (BM + BN) * k binary16 values in and BM * BN floats out (twice with C).
-  double cost = 0.0;
+  // The schedule, as the host build plans it (plan_schedule in
+  // grouped_gemm.cpp): longest processing time first at two levels.  Sorted
+  // positions go whole to the chunk with the least estimated time so far,
+  // longest first (ties: lower position first); within a chunk they run
+  // longest work tile first (ties: lower position first).
+  double total = 0.0, key = 0.0;
   if (pos < experts) {
-    const double r = (double)min(args.cta_m * args.work_tm, rows);
-    const double c = (double)min(args.cta_n * args.work_tn, max(L.n, 0));
-    cost = 2.0 * (r + c) * (double)max(L.k, 0) + 4.0 * r * c * (reads_c ? 2.0 : 1.0);
-    s_cost[pos] = cost;
+    if (work > 0) {
+      const int bm = args.cta_m * args.work_tm, bn = args.cta_n * args.work_tn;
+      total = problem_work_time(rows, L.n, L.k, (rows - 1) / bm + 1, (L.n - 1) / bn + 1, args.stage_k, reads_c);
+      key = total / work;
+    }
+    s_total[pos] = total;
+    s_key[pos] = key;
+    s_work[pos] = work;
   }
-  double sum;
-  const double cum = block_exclusive_scan<double>(cost * (double)work, s_waves_d, &sum);
-  if (pos < experts) s_cum[pos] = cum;
   __syncthreads();
-  if (tid >= 1 && tid < kChunks) {
-    // The first sorted position whose work tiles reach the target cost.
-    const double target = sum * tid / kChunks;
-    int lo = 0, hi = experts;  // answer in [lo, hi]; hi = experts means none
-    while (lo < hi) {
-      const int mid = (lo + hi) / 2;
-      const double end = s_cum[mid] + s_cost[mid] * (double)(s_work_off[mid + 1] - s_work_off[mid]);
-      if (end >= target) hi = mid;
-      else lo = mid + 1;
+  if (pos < experts) {
+    int rank = 0;
+    for (int j = 0; j < experts; ++j) {
+      const double t = s_total[j];
+      rank += (t > total || (t == total && j < pos)) ? 1 : 0;
     }
-    int t = total_work;
-    if (lo < experts) {
-      const double into = s_cost[lo] > 0.0 ? (target - s_cum[lo]) / s_cost[lo] : 0.0;
-      const double room = (double)(s_work_off[lo + 1] - s_work_off[lo]);
-      t = s_work_off[lo] + (int)(into < room ? into : room);
-    }
-    s_bounds[tid] = t < total_work ? t : total_work;
+    s_by_total[rank] = total;
+    s_order[rank] = pos;
   }
   __syncthreads();
   if (tid == 0) {
-    int prev = 0;
+    // Greedy assignment, one position at a time onto the first least-loaded
+    // chunk; the loads stay in registers (a tournament for the minimum).
+    double load[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) load[c] = 0.0;
+    for (int r = 0; r < experts; ++r) {
+      const double t = s_by_total[r];
+      int idx[kChunks];
+      double val[kChunks];
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) {
+        idx[c] = c;
+        val[c] = load[c];
+      }
+#pragma unroll
+      for (int width = kChunks / 2; width >= 1; width /= 2) {
+#pragma unroll
+        for (int c = 0; c < width; ++c) {
+          // ties go to the lower chunk: the first minimum, as a scan finds it
+          const bool right = val[c + width] < val[c] || (val[c + width] == val[c] && idx[c + width] < idx[c]);
+          val[c] = right ? val[c + width] : val[c];
+          idx[c] = right ? idx[c + width] : idx[c];
+        }
+      }
+      const int best = idx[0];
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) load[c] = c == best ? load[c] + t : load[c];
+      s_chunk[s_order[r]] = best;
+    }
+  }
+  __syncthreads();
+  int chunk = 0;
+  if (pos < experts) {
+    chunk = s_chunk[pos];
+    int before = 0;  // positions scheduled ahead of this one
+    for (int j = 0; j < experts; ++j) {
+      const int cj = s_chunk[j];
+      const double kj = s_key[j];
+      before += (cj < chunk || (cj == chunk && (kj > key || (kj == key && j < pos)))) ? 1 : 0;
+    }
+    atomicAdd(&s_chunk_work[chunk], work);
+    s_order[before] = pos;  // its by-total contents were last read by the greedy pass
+  }
+  __syncthreads();
+  int sched_work = 0;
+  if (pos < experts) sched_work = s_work[s_order[pos]];
+  int total_work;
+  const int work_off = block_exclusive_scan<int>(sched_work, s_waves_i, &total_work);
+  if (pos < experts) {
+    args.order[pos] = s_order[pos];
+    args.offsets[experts + 1 + pos] = work_off;
+  }
+  if (tid == 0) {
+    args.offsets[2 * experts + 1] = total_work;
     args.header[0] = total_tiles;
     args.header[1] = total_work;
-    args.header[2] = 0;
-    for (int c = 1; c < kChunks; ++c) {
-      prev = s_bounds[c] > prev ? s_bounds[c] : prev;
-      args.header[2 + c] = prev;
+    int bound = 0;
+    for (int c = 0; c < kChunks; ++c) {
+      args.header[2 + c] = bound;
+      bound += s_chunk_work[c];
     }
-    args.header[2 + kChunks] = total_work;
+    args.header[2 + kChunks] = bound;
     for (int h = 3 + kChunks; h < GGK_MOE_HEADER_INTS; ++h) args.header[h] = 0;
     args.header[GGK_MOE_STATUS] = s_status;
   }
@@ -234,7 +298,7 @@ constexpr int kCta[GGK_VARIANT_COUNT][2] = {{64, 64}, {128, 64}, {64, 128}, {128
 
 extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts,
                                       int sort_mode, gg_device_problem_desc* d_problems, int* d_offsets,
-                                      int* d_sorted_to_original, int* d_header, hipStream_t stream) {
+                                      int* d_sorted_to_original, int* d_order, int* d_header, hipStream_t stream) {
   if (layout == nullptr || variant < 0 || variant >= GGK_VARIANT_COUNT || sort_mode < 0 || sort_mode > 3) {
     return hipErrorInvalidValue;
   }
@@ -255,11 +319,11 @@ extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layou
   const long long col_tiles = ((long long)L.n + cta_n - 1) / cta_n;
   if (row_tiles * col_tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   if (L.a == nullptr || L.b == nullptr || L.d == nullptr || d_counts == nullptr || d_problems == nullptr ||
-      d_offsets == nullptr || d_sorted_to_original == nullptr || d_header == nullptr) {
+      d_offsets == nullptr || d_sorted_to_original == nullptr || d_order == nullptr || d_header == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  MoeArgs args{L, d_counts, sort_mode, cta_m, cta_n, work.tiles_m, work.tiles_n, d_problems, d_offsets,
-               d_sorted_to_original, d_header};
+  MoeArgs args{L,         d_counts,  sort_mode,  cta_m, cta_n, work.tiles_m, work.tiles_n, work.stage_k, d_problems,
+               d_offsets, d_sorted_to_original, d_order, d_header};
   void* params[] = {&args};
   return hipLaunchKernel(reinterpret_cast<const void*>(moe_prepare_kernel), dim3(1), dim3(kThreads), params, 0,
                          stream);

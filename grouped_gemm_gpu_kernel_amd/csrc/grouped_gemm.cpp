@@ -147,20 +147,27 @@ struct Schedule {
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> bounds{};
 };
 
-// Estimated time of one work tile of problem p, in cycles of one CU: a fixed
-// part (finding the tile, the first stage's latency, the claim), a k-loop
-// whose stages cost mostly their latency plus a little per row and column
-// they move, and an epilogue that moves rows x cols floats (twice when C is
-// read).  The constants are a least-squares fit to per-tile clock stamps of
-// the grouped kernel on mixed shapes (median error 7%); only the ratios
-// between problems matter.
-double work_tile_time(const DeviceProblemDesc& p, int bm, int bn, int bk) {
-  if (p.m <= 0 || p.n <= 0) return 0.0;
-  const double rows = static_cast<double>(p.m) / ceil_div(p.m, bm);  // mean rows of the problem's tiles
-  const double cols = static_cast<double>(p.n) / ceil_div(p.n, bn);
-  const double stages = ceil_div(std::max(p.k, 0), bk);
-  const bool reads_c = p.c != nullptr && p.beta != 0.0f;
-  return 15000.0 + stages * (3100.0 + 2.9 * (rows + cols)) + 0.23 * rows * cols * (reads_c ? 2.0 : 1.0);
+// Estimated time of all work tiles of problem p, in hundredths of a cycle of
+// one CU.  Per work tile: a fixed part (finding the tile, the first stage's
+// latency, the claim), a k-loop whose stages cost mostly their latency plus a
+// little per row and column they move, and an epilogue that moves rows x cols
+// floats (twice when C is read):
+//   150 + stages * (31 + 0.029 (rows + cols)) + 0.0023 rows cols  (x 100)
+// The constants are a least-squares fit to per-tile clock stamps of the
+// grouped kernel on mixed shapes (median error 7%); only the ratios between
+// problems matter.  Summed over the tm x tn work tiles, the rows add up to
+// m tn, the columns to n tm and the areas to m n, so the total is a sum of
+// integer products, evaluated in double one operation at a time: the
+// device-side prepare (gg_moe.hip) evaluates the same expression in the same
+// order and gets the same value, hence the same schedule.
+double problem_work_time(int m, int n, int k, int tm, int tn, int bk, bool reads_c) {
+  if (m <= 0 || n <= 0 || tm <= 0 || tn <= 0) return 0.0;
+  const double w = static_cast<double>(tm) * tn;
+  const double stages = k > 0 ? (k - 1) / bk + 1 : 0;
+  const double edge = static_cast<double>(m) * tn + static_cast<double>(n) * tm;
+  const double stage = 310000.0 * w + 290.0 * edge;
+  const double area = static_cast<double>(m) * n;
+  return 1500000.0 * w + stages * stage + (reads_c ? 46.0 : 23.0) * area;
 }
 
 // Longest processing time first at two levels.  Problems go whole to the XCD
@@ -175,8 +182,12 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
   const int count = static_cast<int>(problems.size());
   std::vector<double> tile_time(count), total(count);
   for (int i = 0; i < count; ++i) {
-    tile_time[i] = work[i] > 0 ? work_tile_time(problems[i], bm, bn, bk) : 0.0;
-    total[i] = tile_time[i] * work[i];
+    const DeviceProblemDesc& p = problems[i];
+    const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+    const int tm = p.m > 0 ? (p.m - 1) / bm + 1 : 0;  // work tiles along M and N
+    const int tn = p.n > 0 ? (p.n - 1) / bn + 1 : 0;
+    total[i] = work[i] > 0 ? problem_work_time(p.m, p.n, p.k, tm, tn, bk, reads_c) : 0.0;
+    tile_time[i] = work[i] > 0 ? total[i] / work[i] : 0.0;
   }
   std::vector<int> by_total(count);
   for (int i = 0; i < count; ++i) by_total[i] = i;
@@ -562,12 +573,13 @@ struct MoeGroupedGemm::Impl {
   int sort_mode = 0;
   int grid_ctas = 0;
   DeviceProblemDesc* d_problems = nullptr;
-  int* d_ints = nullptr;  // offsets [2 * (E + 1)] | permutation [E] | header | scheduler state
+  int* d_ints = nullptr;  // offsets [2 * (E + 1)] | permutation [E] | order [E] | header
   int* d_state = nullptr;
 
   int* offsets() const { return d_ints; }
   int* perm() const { return d_ints + 2 * (layout.experts + 1); }
-  int* header() const { return perm() + layout.experts; }
+  int* order() const { return perm() + layout.experts; }
+  int* header() const { return order() + layout.experts; }
 };
 
 MoeGroupedGemm::MoeGroupedGemm() : impl_(new Impl()) {}
@@ -643,7 +655,7 @@ hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& co
   if (wide < 0) return hipErrorInvalidValue;
 
   release(impl_->d_problems, impl_->d_ints, impl_->d_state);
-  const size_t ints = 2 * static_cast<size_t>(e + 1) + e + GGK_MOE_HEADER_INTS;
+  const size_t ints = 2 * static_cast<size_t>(e + 1) + 2 * static_cast<size_t>(e) + GGK_MOE_HEADER_INTS;
   status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems), e * sizeof(DeviceProblemDesc));
   if (status != hipSuccess) return status;
   status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_ints), ints * sizeof(int));
@@ -675,11 +687,13 @@ hipError_t MoeGroupedGemm::run(const int* d_counts, hipStream_t stream) const {
   if (impl_ == nullptr || impl_->d_problems == nullptr) return hipErrorInvalidDevicePointer;
   if (d_counts == nullptr) return hipErrorInvalidDevicePointer;
   hipError_t status = ggk_moe_prepare(impl_->variant, impl_->path, &impl_->layout, d_counts, impl_->sort_mode,
-                                      impl_->d_problems, impl_->offsets(), impl_->perm(), impl_->header(), stream);
+                                      impl_->d_problems, impl_->offsets(), impl_->perm(), impl_->order(),
+                                      impl_->header(), stream);
   if (status != hipSuccess) return status;
   return ggk_launch_grouped_device(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                                   impl_->offsets() + impl_->layout.experts + 1, impl_->layout.experts,
-                                   impl_->header(), impl_->d_state, impl_->grid_ctas, stream);
+                                   impl_->offsets() + impl_->layout.experts + 1, impl_->order(),
+                                   impl_->layout.experts, impl_->header(), impl_->d_state, impl_->grid_ctas,
+                                   stream);
 }
 
 int MoeGroupedGemm::grid_ctas() const { return impl_ != nullptr ? impl_->grid_ctas : 0; }
@@ -690,6 +704,7 @@ const int* MoeGroupedGemm::device_offsets() const { return impl_ != nullptr && i
 const int* MoeGroupedGemm::device_sorted_to_original() const {
   return impl_ != nullptr && impl_->d_ints ? impl_->perm() : nullptr;
 }
+const int* MoeGroupedGemm::device_order() const { return impl_ != nullptr && impl_->d_ints ? impl_->order() : nullptr; }
 const int* MoeGroupedGemm::device_header() const { return impl_ != nullptr && impl_->d_ints ? impl_->header() : nullptr; }
 
 }  // namespace grouped_gemm

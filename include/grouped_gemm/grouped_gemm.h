@@ -236,10 +236,12 @@ class MoeGroupedGemm {
   int grid_ctas() const;
   // The prepared set as the last run wrote it (device memory, stream order):
   // experts descriptors, 2 * (experts + 1) offsets (reference tiles, then work
-  // tiles), the permutation, and GGK_MOE_HEADER_INTS header ints.
+  // tiles in scheduling order), the permutation, the scheduling order
+  // (experts sorted positions) and GGK_MOE_HEADER_INTS header ints.
   const DeviceProblemDesc* device_problems() const;
   const int* device_offsets() const;
   const int* device_sorted_to_original() const;
+  const int* device_order() const;
   const int* device_header() const;
 
  private:

@@ -144,14 +144,14 @@ int gg_grid_ctas_for(const gg_kernel_config* config, int total_tiles);
  * ggk_moe_prepare for the layout.  gg_moe_create checks the layout and
  * allocates once; gg_moe_run launches prepare + grouped kernel on the stream
  * with no host synchronisation or allocation (capturable in a HIP graph).
- * gg_moe_device_buffers returns the device-side prepared set (any output may
- * be NULL). */
+ * gg_moe_device_buffers returns the device-side prepared set, the scheduling
+ * order last (any output may be NULL). */
 typedef struct gg_moe gg_moe;
 int gg_moe_create(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode, gg_moe** out);
 int gg_moe_run(const gg_moe* moe, const int* d_counts, hipStream_t stream);
 int gg_moe_grid_ctas(const gg_moe* moe);
 int gg_moe_device_buffers(const gg_moe* moe, const gg_device_problem_desc** problems, const int** offsets,
-                          const int** sorted_to_original, const int** header);
+                          const int** sorted_to_original, const int** header, const int** order);
 void gg_moe_destroy(gg_moe* moe);
 
 #ifdef __cplusplus

@@ -203,9 +203,13 @@ hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
  * synchronisation: d_problems[E], the descriptors in the order
  * prepare_problem_set gives for sort_mode (src/grouped_gemm.cu:967-1022);
  * d_offsets[2 * (E + 1)], the reference tile offsets then the work-tile
- * offsets; d_sorted_to_original[E]; and d_header[GGK_MOE_HEADER_INTS]:
- * [0] total tiles, [1] total work tiles, [2, 2 + GGK_SCHEDULER_CHUNKS] the
- * chunk bounds, [GGK_MOE_STATUS] status bits.  Counts are not trusted: a
+ * offsets in scheduling order; d_sorted_to_original[E]; d_order[E], the
+ * sorted position at each scheduling position; and
+ * d_header[GGK_MOE_HEADER_INTS]: [0] total tiles, [1] total work tiles,
+ * [2, 2 + GGK_SCHEDULER_CHUNKS] the chunk bounds, [GGK_MOE_STATUS] status
+ * bits.  The schedule (order, work-tile offsets, chunk bounds) is the one
+ * GroupedGemmExecutor::build plans for the same descriptors: longest
+ * processing time first, whole problems per chunk.  Counts are not trusted: a
  * negative count is taken as 0 (GGK_MOE_NEGATIVE) and rows at or past
  * max_rows are dropped (GGK_MOE_CLAMPED), so no launch touches rows outside
  * [0, max_rows) of A, C and D.  1 <= E <= GGK_MOE_MAX_EXPERTS. */
@@ -234,16 +238,17 @@ typedef struct ggk_moe_layout {
 
 hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts, int sort_mode,
                            gg_device_problem_desc* d_problems, int* d_offsets, int* d_sorted_to_original,
-                           int* d_header, hipStream_t stream);
+                           int* d_order, int* d_header, hipStream_t stream);
 
 /* The grouped launch of a device-prepared set: the same kernel as
  * ggk_launch_grouped, which reads the work-tile total and the chunk bounds
  * from d_header (as ggk_moe_prepare writes it) when it starts.  grid is fixed
  * by the caller (e.g. every resident workgroup); workgroups that find no work
- * retire at once. */
+ * retire at once.  d_order as for ggk_launch_grouped (NULL: scheduling order
+ * = descriptor order). */
 hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
-                                     const int* d_work_offsets, int problem_count, const int* d_header,
-                                     int* d_state, int grid, hipStream_t stream);
+                                     const int* d_work_offsets, const int* d_order, int problem_count,
+                                     const int* d_header, int* d_state, int grid, hipStream_t stream);
 
 /* One problem, one workgroup per work tile, row-major work-tile order
  * (single_problem_gemm_kernel + launch_single_problem_variant,

@@ -2,8 +2,8 @@
 
 The prepared set it writes on the GPU must equal, bit for bit, what the host path gives for the same
 problems: prepare_problem_set's permutation and tile offsets (src/grouped_gemm.cu:967-1022, itself
-pinned to the oracle and the reference's published rows), the descriptors build() uploads and the
-work-tile offsets.  D must equal the host path's D bit for bit (same kernel, same tiles) and the
+pinned to the oracle and the reference's published rows), the descriptors build() uploads, and the
+schedule build() plans (longest processing time first, restated below in _plan_schedule).  D must equal the host path's D bit for bit (same kernel, same tiles) and the
 oracle's host GEMM within 1e-3*sqrt(K)*max|A|*max|B|*|alpha| + 1e-6*(|beta|*max|C| + 1).  Counts are
 untrusted input: negative or oversubscribed counts are clamped and reported, never read or written
 out of bounds.  Runs are captured in a graph and replayed with new counts."""
@@ -46,15 +46,15 @@ def test_invalid_layouts_rejected_on_host():
     lay = _lib.GGKMoeLayout(0, 64, 64, 0x1000, 64, 0x2000, 64, 64 * 64, None, 64, 0x3000, 64, 1.0, 0.0, 100)
     buf = ctypes.c_void_p(0x4000)
     L = _lib.lib()
-    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, None) == 1  # experts = 0
+    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1  # experts = 0
     lay.experts = _lib.GGK_MOE_MAX_EXPERTS + 1
-    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, None) == 1
+    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1
     lay.experts = 4
     lay.lda = 10  # below K
-    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, None) == 1
+    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1
     lay.lda = 64
-    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 7, buf, buf, buf, buf, None) == 1  # sort mode
-    assert L.ggk_moe_prepare(5, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, None) == 1  # variant
+    assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 7, buf, buf, buf, buf, buf, None) == 1  # sort mode
+    assert L.ggk_moe_prepare(5, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1  # variant
 
 
 # ---------------------------------------------------------------- GPU
@@ -99,18 +99,56 @@ def _host_problems(a, b, c, d, counts, alpha, beta, max_rows):
 
 
 def _read_device_set(plan, experts):
-    probs_ptr, offs_ptr, perm_ptr, head_ptr = plan.moe.device_buffers()
+    probs_ptr, offs_ptr, perm_ptr, head_ptr, order_ptr = plan.moe.device_buffers()
     L = _lib.lib()
     descs = (_lib.GGDeviceProblemDesc * experts)()
     offs = np.zeros(2 * (experts + 1), np.int32)
     perm = np.zeros(experts, np.int32)
+    order = np.zeros(experts, np.int32)
     head = np.zeros(_lib.GGK_MOE_HEADER_INTS, np.int32)
     torch.cuda.synchronize()
     for dst, src, nbytes in ((ctypes.addressof(descs), probs_ptr, ctypes.sizeof(descs)),
                              (offs.ctypes.data, offs_ptr, offs.nbytes), (perm.ctypes.data, perm_ptr, perm.nbytes),
-                             (head.ctypes.data, head_ptr, head.nbytes)):
+                             (order.ctypes.data, order_ptr, order.nbytes), (head.ctypes.data, head_ptr, head.nbytes)):
         _lib.check(L.ggk_copy_to_host(dst, src, nbytes), "copy")
-    return descs, offs, perm, head
+    return descs, offs, perm, order, head
+
+
+def _plan_schedule(shapes, work, bm, bn, bk, reads_c):
+    """The host build's schedule (plan_schedule, csrc/grouped_gemm.cpp) for problems in sorted order:
+    shapes[i] = (m, n, k), work[i] work tiles of bm x bn.  Estimated time of a problem in hundredths
+    of a cycle: sum over its tm x tn work tiles of 150 + stages (31 + 0.029 (rows + cols)) +
+    0.0023 rows cols (x2 with C), i.e. 1500000 W + stages (310000 W + 290 (m tn + n tm)) + 23 m n (46
+    with C), each operation rounded in double.  Problems go whole, longest first (stable), to the
+    first least-loaded of the 8 chunks; within a chunk, longest work tile first, then position.
+    Returns (order, work offsets in that order, chunk bounds)."""
+    count = len(shapes)
+    total, key = [0.0] * count, [0.0] * count
+    for i, ((m, n, k), w) in enumerate(zip(shapes, work)):
+        if w <= 0:
+            continue
+        tm, tn = (m - 1) // bm + 1, (n - 1) // bn + 1
+        wt = float(tm) * tn
+        stages = float((k - 1) // bk + 1) if k > 0 else 0.0
+        edge = float(m) * tn + float(n) * tm
+        stage = 310000.0 * wt + 290.0 * edge
+        area = float(m) * n
+        total[i] = 1500000.0 * wt + stages * stage + (46.0 if reads_c else 23.0) * area
+        key[i] = total[i] / w
+    chunks = _lib.GGK_SCHEDULER_CHUNKS
+    load = [0.0] * chunks
+    members = [[] for _ in range(chunks)]
+    for i in sorted(range(count), key=lambda i: -total[i]):
+        c = min(range(chunks), key=lambda d: load[d])  # the first least-loaded chunk
+        load[c] += total[i]
+        members[c].append(i)
+    order, offsets, bounds = [], [0], [0]
+    for c in range(chunks):
+        for i in sorted(members[c], key=lambda i: (-key[i], i)):
+            order.append(i)
+            offsets.append(offsets[-1] + work[i])
+        bounds.append(offsets[-1])
+    return order, offsets, bounds
 
 
 @pytest.mark.gpu
@@ -129,12 +167,12 @@ def test_device_prepare_equals_host_prepare(torch_cuda, config, experts):
     for mode in SortMode:
         plan = torch_ops.MoeGroupedGemmPlan(a, b, d, c, 1.5, 0.5, sort_mode=mode, config=cfg)
         plan.run(counts_dev)
-        descs, offs, perm, head = _read_device_set(plan, experts)
+        descs, offs, perm, order, head = _read_device_set(plan, experts)
         probs = _host_problems(a, b, c, d, counts, 1.5, 0.5, rows)
         prep = api.prepare_problem_set(probs, cfg, mode)
         assert list(perm) == prep.sorted_to_original, (config, experts, mode)
         assert list(offs[:experts + 1]) == prep.tile_offsets, (config, experts, mode)
-        work = [0]
+        work = []
         for i, p in enumerate(prep.sorted_problems):
             dd = descs[i]
             tm = -(-p.m // cfg.cta_m) if p.m > 0 and p.n > 0 else 0
@@ -143,11 +181,15 @@ def test_device_prepare_equals_host_prepare(torch_cuda, config, experts):
                    dd.alpha, dd.beta, dd.tiles_m, dd.tiles_n)
             want = (p.m, p.n, p.k, p.a, p.b, p.c or 0, p.d, p.lda, p.ldb, p.ldc, p.ldd, p.alpha, p.beta, tm, tn)
             assert got == want, (config, experts, mode, i)
-            work.append(work[-1] + (-(-tm // shape.tiles_m)) * (-(-tn // shape.tiles_n)))
-        assert list(offs[experts + 1:]) == work
-        assert head[0] == prep.total_tiles and head[1] == work[-1]
-        bounds = list(head[2:2 + _lib.GGK_SCHEDULER_CHUNKS + 1])
-        assert bounds[0] == 0 and bounds[-1] == work[-1] and bounds == sorted(bounds)
+            work.append((-(-tm // shape.tiles_m)) * (-(-tn // shape.tiles_n)))
+        want_order, want_offsets, want_bounds = _plan_schedule(
+            [(p.m, p.n, p.k) for p in prep.sorted_problems], work, cfg.cta_m * shape.tiles_m,
+            cfg.cta_n * shape.tiles_n, shape.stage_k, True)
+        assert sorted(want_order) == list(range(experts))
+        assert list(order) == want_order, (config, experts, mode)
+        assert list(offs[experts + 1:]) == want_offsets, (config, experts, mode)
+        assert head[0] == prep.total_tiles and head[1] == sum(work)
+        assert list(head[2:2 + _lib.GGK_SCHEDULER_CHUNKS + 1]) == want_bounds, (config, experts, mode)
         assert head[_lib.GGK_MOE_STATUS] == 0
         plan.close()
 

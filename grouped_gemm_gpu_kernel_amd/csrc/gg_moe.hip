@@ -22,6 +22,9 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
 constexpr int kMaxExperts = GGK_MOE_MAX_EXPERTS;
 static_assert(kMaxExperts <= kThreads, "one thread per expert");
+static_assert(kMaxExperts % 4 == 0, "per-expert arrays are read four entries at a time");
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef double double2v __attribute__((ext_vector_type(2)));
 static_assert(kWaves <= kWave, "wave totals are scanned by one wave");
 static_assert(2 + kChunks < GGK_MOE_STATUS && GGK_MOE_STATUS < GGK_MOE_HEADER_INTS, "header layout");
 
@@ -56,6 +59,11 @@ __device__ double problem_work_time(int m, int n, int k, int tm, int tn, int bk,
   return 1500000.0 * w + stages * stage + (reads_c ? 46.0 : 23.0) * area;
 }
 
+// A problem's estimated time as the integer the schedule ranks and adds up:
+// clamped to 2^52, so that up to GGK_MOE_MAX_EXPERTS of them sum exactly in
+// 64 bits (below 2^53 the double is an exact integer already).
+__device__ long long problem_time_units(double t) { return t < 4503599627370496.0 ? (long long)t : (1LL << 52); }
+
 // Exclusive prefix sum of one value per thread over the workgroup, in thread
 // order; *total receives the sum.  Every thread must call it.
 template <class T>
@@ -89,14 +97,14 @@ __device__ T block_exclusive_scan(T v, T* s_waves, T* total) {
 __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   __shared__ long long s_waves_ll[kWaves];
   __shared__ int s_waves_i[kWaves];
-  __shared__ int s_rows[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) int s_rows[kMaxExperts];
   __shared__ long long s_row0[kMaxExperts];
-  __shared__ int s_tiles[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) int s_tiles[kMaxExperts];
   __shared__ int s_perm[kMaxExperts];
-  __shared__ double s_total[kMaxExperts];    // estimated time of sorted position i
-  __shared__ double s_key[kMaxExperts];      // the same per work tile
-  __shared__ double s_by_total[kMaxExperts]; // estimated times, longest first
-  __shared__ int s_chunk[kMaxExperts];       // chunk of sorted position i
+  __shared__ long long s_total[kMaxExperts];    // estimated time of sorted position i (clamped units)
+  __shared__ __attribute__((aligned(16))) double s_key[kMaxExperts];  // estimated time per work tile
+  __shared__ long long s_by_total[kMaxExperts]; // estimated times, longest first
+  __shared__ __attribute__((aligned(16))) int s_chunk[kMaxExperts];  // chunk of sorted position i
   __shared__ int s_order[kMaxExperts];       // sorted position at each scheduling position
   __shared__ int s_work[kMaxExperts];        // work tiles of sorted position i
   __shared__ int s_chunk_work[kChunks];
@@ -145,13 +153,21 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
       const int my_tiles = s_tiles[tid];
       const long long my_area = (long long)s_rows[tid] * L.n;
       rank = 0;
-      for (int j = 0; j < experts; ++j) {
-        const int t = s_tiles[j];
-        const long long area = (long long)s_rows[j] * L.n;
-        const bool by_tiles = tiles_first && t != my_tiles;
-        const bool before = by_tiles ? t > my_tiles : area > my_area;
-        const bool tie = !by_tiles && area == my_area;
-        rank += (before || (tie && j < tid)) ? 1 : 0;
+      // Four experts per step (16-byte LDS reads; entries past E are never counted).
+#pragma unroll 2
+      for (int j0 = 0; j0 < experts; j0 += 4) {
+        const int4v t4 = *reinterpret_cast<const int4v*>(&s_tiles[j0]);
+        const int4v r4 = *reinterpret_cast<const int4v*>(&s_rows[j0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + e;
+          const int t = t4[e];
+          const long long area = (long long)r4[e] * L.n;
+          const bool by_tiles = tiles_first && t != my_tiles;
+          const bool before = by_tiles ? t > my_tiles : area > my_area;
+          const bool tie = !by_tiles && area == my_area;
+          rank += (j < experts && (before || (tie && j < tid))) ? 1 : 0;
+        }
       }
     }
     s_perm[rank] = tid;
@@ -201,12 +217,15 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   // positions go whole to the chunk with the least estimated time so far,
   // longest first (ties: lower position first); within a chunk they run
   // longest work tile first (ties: lower position first).
-  double total = 0.0, key = 0.0;
+  long long total = 0;  // estimated time, clamped (problem_time_units)
+  double key = 0.0;     // estimated time per work tile
   if (pos < experts) {
     if (work > 0) {
       const int bm = args.cta_m * args.work_tm, bn = args.cta_n * args.work_tn;
-      total = problem_work_time(rows, L.n, L.k, (rows - 1) / bm + 1, (L.n - 1) / bn + 1, args.stage_k, reads_c);
-      key = total / work;
+      const double t =
+          problem_work_time(rows, L.n, L.k, (rows - 1) / bm + 1, (L.n - 1) / bn + 1, args.stage_k, reads_c);
+      total = problem_time_units(t);
+      key = t / work;
     }
     s_total[pos] = total;
     s_key[pos] = key;
@@ -215,43 +234,48 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   __syncthreads();
   if (pos < experts) {
     int rank = 0;
+#pragma unroll 8
     for (int j = 0; j < experts; ++j) {
-      const double t = s_total[j];
+      const long long t = s_total[j];
       rank += (t > total || (t == total && j < pos)) ? 1 : 0;
     }
     s_by_total[rank] = total;
     s_order[rank] = pos;
   }
   __syncthreads();
-  if (tid == 0) {
-    // Greedy assignment, one position at a time onto the first least-loaded
-    // chunk; the loads stay in registers (a tournament for the minimum).
-    double load[kChunks];
+  if (tid < kWave) {
+    // Greedy assignment by wave 0, one position at a time onto the first
+    // least-loaded chunk.  The loads are exact integers, uniform across the
+    // wave (scalar registers); the estimated times come from LDS 64 at a
+    // time, one per lane, and each step takes its own from its lane.
+    const int lane = tid;
+    long long load[kChunks];
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) load[c] = 0.0;
-    for (int r = 0; r < experts; ++r) {
-      const double t = s_by_total[r];
-      int idx[kChunks];
-      double val[kChunks];
+    for (int c = 0; c < kChunks; ++c) load[c] = 0;
+    for (int r0 = 0; r0 < experts; r0 += kWave) {
+      const int r = r0 + lane;
+      const long long mine = r < experts ? s_by_total[r] : 0;
+      const int lo = (int)(unsigned long long)mine;
+      const int hi = (int)((unsigned long long)mine >> 32);
+      const int steps = min(kWave, experts - r0);
+      int chosen = 0;  // lane j: the chunk of by-total rank r0 + j
+      for (int j = 0; j < steps; ++j) {
+        const long long t = (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane(hi, j) << 32) |
+                                        (unsigned)__builtin_amdgcn_readlane(lo, j));
+        int best = 0;
+        long long least = load[0];
 #pragma unroll
-      for (int c = 0; c < kChunks; ++c) {
-        idx[c] = c;
-        val[c] = load[c];
-      }
-#pragma unroll
-      for (int width = kChunks / 2; width >= 1; width /= 2) {
-#pragma unroll
-        for (int c = 0; c < width; ++c) {
-          // ties go to the lower chunk: the first minimum, as a scan finds it
-          const bool right = val[c + width] < val[c] || (val[c + width] == val[c] && idx[c + width] < idx[c]);
-          val[c] = right ? val[c + width] : val[c];
-          idx[c] = right ? idx[c + width] : idx[c];
+        for (int c = 1; c < kChunks; ++c) {
+          if (load[c] < least) {  // strict: ties stay with the lower chunk
+            least = load[c];
+            best = c;
+          }
         }
-      }
-      const int best = idx[0];
 #pragma unroll
-      for (int c = 0; c < kChunks; ++c) load[c] = c == best ? load[c] + t : load[c];
-      s_chunk[s_order[r]] = best;
+        for (int c = 0; c < kChunks; ++c) load[c] = c == best ? load[c] + t : load[c];
+        chosen = lane == j ? best : chosen;
+      }
+      if (r < experts) s_chunk[s_order[r]] = chosen;
     }
   }
   __syncthreads();
@@ -259,10 +283,19 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   if (pos < experts) {
     chunk = s_chunk[pos];
     int before = 0;  // positions scheduled ahead of this one
-    for (int j = 0; j < experts; ++j) {
-      const int cj = s_chunk[j];
-      const double kj = s_key[j];
-      before += (cj < chunk || (cj == chunk && (kj > key || (kj == key && j < pos)))) ? 1 : 0;
+#pragma unroll 2
+    for (int j0 = 0; j0 < experts; j0 += 4) {
+      const int4v c4 = *reinterpret_cast<const int4v*>(&s_chunk[j0]);
+      const double2v k01 = *reinterpret_cast<const double2v*>(&s_key[j0]);
+      const double2v k23 = *reinterpret_cast<const double2v*>(&s_key[j0 + 2]);
+      const double kj[4] = {k01[0], k01[1], k23[0], k23[1]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j0 + e;
+        const int cj = c4[e];
+        before += (j < experts && (cj < chunk || (cj == chunk && (kj[e] > key || (kj[e] == key && j < pos))))) ? 1
+                                                                                                             : 0;
+      }
     }
     atomicAdd(&s_chunk_work[chunk], work);
     s_order[before] = pos;  // its by-total contents were last read by the greedy pass

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <array>
+#include <cstdint>
 #include <cstring>
 #include <numeric>
 #include <tuple>
@@ -170,6 +171,12 @@ double problem_work_time(int m, int n, int k, int tm, int tn, int bk, bool reads
   return 1500000.0 * w + stages * stage + (reads_c ? 46.0 : 23.0) * area;
 }
 
+// A problem's estimated time as the integer the schedule ranks and adds up:
+// clamped to 2^52 (below 2^53 the double is an exact integer already), so
+// that up to 2^11 of them sum exactly in 64 bits; the chunk loads saturate
+// beyond that.
+int64_t problem_time_units(double t) { return t < 4503599627370496.0 ? static_cast<int64_t>(t) : (int64_t{1} << 52); }
+
 // Longest processing time first at two levels.  Problems go whole to the XCD
 // chunk with the least estimated work so far, largest problems first (a
 // problem's tiles share A and B panels, which that XCD's L2 then serves);
@@ -180,26 +187,28 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
                        int bk) {
   constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
   const int count = static_cast<int>(problems.size());
-  std::vector<double> tile_time(count), total(count);
+  std::vector<double> tile_time(count);
+  std::vector<int64_t> total(count);
   for (int i = 0; i < count; ++i) {
     const DeviceProblemDesc& p = problems[i];
     const bool reads_c = p.c != nullptr && p.beta != 0.0f;
     const int tm = p.m > 0 ? (p.m - 1) / bm + 1 : 0;  // work tiles along M and N
     const int tn = p.n > 0 ? (p.n - 1) / bn + 1 : 0;
-    total[i] = work[i] > 0 ? problem_work_time(p.m, p.n, p.k, tm, tn, bk, reads_c) : 0.0;
-    tile_time[i] = work[i] > 0 ? total[i] / work[i] : 0.0;
+    const double t = work[i] > 0 ? problem_work_time(p.m, p.n, p.k, tm, tn, bk, reads_c) : 0.0;
+    total[i] = problem_time_units(t);
+    tile_time[i] = work[i] > 0 ? t / work[i] : 0.0;
   }
   std::vector<int> by_total(count);
   for (int i = 0; i < count; ++i) by_total[i] = i;
   std::stable_sort(by_total.begin(), by_total.end(), [&](int x, int y) { return total[x] > total[y]; });
-  std::array<double, kChunks> load{};
+  std::array<int64_t, kChunks> load{};
   std::array<std::vector<int>, kChunks> members;
   for (const int i : by_total) {
     int c = 0;
     for (int d = 1; d < kChunks; ++d) {
       if (load[d] < load[c]) c = d;
     }
-    load[c] += total[i];
+    load[c] = load[c] > INT64_MAX - total[i] ? INT64_MAX : load[c] + total[i];
     members[c].push_back(i);
   }
   Schedule s;

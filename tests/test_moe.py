@@ -119,11 +119,12 @@ def _plan_schedule(shapes, work, bm, bn, bk, reads_c):
     shapes[i] = (m, n, k), work[i] work tiles of bm x bn.  Estimated time of a problem in hundredths
     of a cycle: sum over its tm x tn work tiles of 150 + stages (31 + 0.029 (rows + cols)) +
     0.0023 rows cols (x2 with C), i.e. 1500000 W + stages (310000 W + 290 (m tn + n tm)) + 23 m n (46
-    with C), each operation rounded in double.  Problems go whole, longest first (stable), to the
-    first least-loaded of the 8 chunks; within a chunk, longest work tile first, then position.
+    with C), each operation rounded in double, then taken as an integer clamped to 2^52.  Problems go
+    whole, longest first (stable), to the first least-loaded of the 8 chunks (integer loads); within
+    a chunk, longest work tile (unclamped time / W) first, then position.
     Returns (order, work offsets in that order, chunk bounds)."""
     count = len(shapes)
-    total, key = [0.0] * count, [0.0] * count
+    total, key = [0] * count, [0.0] * count
     for i, ((m, n, k), w) in enumerate(zip(shapes, work)):
         if w <= 0:
             continue
@@ -133,10 +134,11 @@ def _plan_schedule(shapes, work, bm, bn, bk, reads_c):
         edge = float(m) * tn + float(n) * tm
         stage = 310000.0 * wt + 290.0 * edge
         area = float(m) * n
-        total[i] = 1500000.0 * wt + stages * stage + (46.0 if reads_c else 23.0) * area
-        key[i] = total[i] / w
+        t = 1500000.0 * wt + stages * stage + (46.0 if reads_c else 23.0) * area
+        total[i] = int(t) if t < 2.0 ** 52 else 1 << 52
+        key[i] = t / w
     chunks = _lib.GGK_SCHEDULER_CHUNKS
-    load = [0.0] * chunks
+    load = [0] * chunks
     members = [[] for _ in range(chunks)]
     for i in sorted(range(count), key=lambda i: -total[i]):
         c = min(range(chunks), key=lambda d: load[d])  # the first least-loaded chunk

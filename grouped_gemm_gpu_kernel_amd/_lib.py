@@ -133,6 +133,7 @@ SIGNATURES = {
     "gg_executor_total_tiles": (_i, [_vp]),
     "gg_executor_grid_ctas": (_i, [_vp]),
     "gg_executor_using_tensor_cores": (_i, [_vp]),
+    "gg_executor_schedule": (_i, [_vp, _P(GGKWorkShape), _vp, _vp, _vp]),
     "gg_run_grouped_gemm_once": (_i, [_P(GGProblemDesc), _i, _i, _P(GGKernelConfig), _vp]),
     "gg_run_baseline_per_problem": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _vp]),
     "gg_count_non_empty_problems": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig)]),

@@ -225,6 +225,18 @@ class GroupedGemmExecutor:
     def using_tensor_cores(self) -> bool:
         return bool(_lib.lib().gg_executor_using_tensor_cores(self._handle))
 
+    def schedule(self):
+        """(work shape, scheduling order, work-tile offsets in that order, chunk bounds) as build()
+        planned them (no reference counterpart)."""
+        count = self.problem_count()
+        shape = _lib.GGKWorkShape()
+        order = (ctypes.c_int * max(1, count))()
+        offsets = (ctypes.c_int * (count + 1))()
+        bounds = (ctypes.c_int * (_lib.GGK_SCHEDULER_CHUNKS + 1))()
+        _lib.check(_lib.lib().gg_executor_schedule(self._handle, ctypes.byref(shape), order, offsets, bounds),
+                   "gg_executor_schedule")
+        return shape, list(order)[:count], list(offsets), list(bounds)
+
 
 @dataclass
 class MoeLayout:

@@ -5,6 +5,7 @@
 // as int.  No exception crosses this boundary.
 #include "grouped_gemm_amd.h"
 
+#include <algorithm>
 #include <cstddef>
 #include <new>
 #include <vector>
@@ -209,6 +210,18 @@ int gg_executor_grid_ctas(const gg_executor* executor) {
 
 int gg_executor_using_tensor_cores(const gg_executor* executor) {
   return executor != nullptr && executor->executor.using_tensor_cores() ? 1 : 0;
+}
+
+int gg_executor_schedule(const gg_executor* executor, ggk_work_shape* shape, int* order, int* work_offsets,
+                         int* chunk_bounds) {
+  if (executor == nullptr) return hipErrorInvalidDevicePointer;
+  std::vector<int> o, w, b;
+  const hipError_t status = executor->executor.schedule(shape, &o, &w, &b);
+  if (status != hipSuccess) return status;
+  if (order != nullptr) std::copy(o.begin(), o.end(), order);
+  if (work_offsets != nullptr) std::copy(w.begin(), w.end(), work_offsets);
+  if (chunk_bounds != nullptr) std::copy(b.begin(), b.end(), chunk_bounds);
+  return hipSuccess;
 }
 
 int gg_run_grouped_gemm_once(const gg_problem_desc* problems, int count, int sort_mode,

@@ -534,6 +534,33 @@ bool GroupedGemmExecutor::using_tensor_cores() const {
   return impl_ != nullptr && impl_->path == GGK_PATH_MFMA;
 }
 
+hipError_t GroupedGemmExecutor::schedule(ggk_work_shape* shape, std::vector<int>* order,
+                                         std::vector<int>* work_offsets, std::vector<int>* chunk_bounds) const {
+  if (impl_ == nullptr || impl_->variant < 0) return hipErrorInvalidDevicePointer;
+  const int count = impl_->problem_count;
+  if (shape != nullptr) {
+    const hipError_t status = ggk_work_shape_get(impl_->variant, impl_->path, shape);
+    if (status != hipSuccess) return status;
+  }
+  // Device ints: [count + 1] reference tile offsets, [count + 1] work-tile
+  // offsets, [count] scheduling order.
+  std::vector<int> ints(count > 0 ? 3 * static_cast<size_t>(count) + 2 : 0);
+  if (count > 0) {
+    const hipError_t status = ggk_copy_to_host(ints.data(), impl_->d_tile_offsets, ints.size() * sizeof(int));
+    if (status != hipSuccess) return status;
+  }
+  if (work_offsets != nullptr) {
+    work_offsets->assign(1, 0);
+    if (count > 0) work_offsets->assign(ints.begin() + count + 1, ints.begin() + 2 * count + 2);
+  }
+  if (order != nullptr) {
+    order->clear();
+    if (count > 0) order->assign(ints.begin() + 2 * count + 2, ints.end());
+  }
+  if (chunk_bounds != nullptr) chunk_bounds->assign(impl_->chunk_bounds.begin(), impl_->chunk_bounds.end());
+  return hipSuccess;
+}
+
 // run_grouped_gemm_once (src/grouped_gemm.cu:1279-1291).
 hipError_t run_grouped_gemm_once(const std::vector<ProblemDesc>& problems, SortMode sort_mode,
                                  const KernelConfig& config, hipStream_t stream) {

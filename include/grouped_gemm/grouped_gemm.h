@@ -154,6 +154,12 @@ class GroupedGemmExecutor {
   // scheduler with instrumentation (see ggk_launch_grouped_traced).
   hipError_t run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream = nullptr) const;
   bool using_tensor_cores() const;
+  // The schedule build() planned: the work-tile shape of the kernel it chose,
+  // the scheduling order (sorted position at each scheduling position), the
+  // work-tile offsets in that order and the per-XCD chunk bounds.  Reads the
+  // device copy back (synchronous); any output may be null.
+  hipError_t schedule(ggk_work_shape* shape, std::vector<int>* order, std::vector<int>* work_offsets,
+                      std::vector<int>* chunk_bounds) const;
 
  private:
   struct Impl;

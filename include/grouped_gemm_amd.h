@@ -122,6 +122,11 @@ int gg_executor_problem_count(const gg_executor* executor);
 int gg_executor_total_tiles(const gg_executor* executor);
 int gg_executor_grid_ctas(const gg_executor* executor);
 int gg_executor_using_tensor_cores(const gg_executor* executor);
+/* GroupedGemmExecutor::schedule (no reference counterpart): work-tile shape,
+ * order[problem_count], work_offsets[problem_count + 1],
+ * chunk_bounds[GGK_SCHEDULER_CHUNKS + 1]; any output may be NULL. */
+int gg_executor_schedule(const gg_executor* executor, ggk_work_shape* shape, int* order, int* work_offsets,
+                         int* chunk_bounds);
 
 /* run_grouped_gemm_once (src/grouped_gemm.cu:1279-1291). */
 int gg_run_grouped_gemm_once(const gg_problem_desc* problems, int count, int sort_mode,

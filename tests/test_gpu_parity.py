@@ -21,6 +21,7 @@ from grouped_gemm_gpu_kernel_amd import _lib, api
 from grouped_gemm_gpu_kernel_amd.api import GroupedGemmExecutor, KernelConfig, ProblemDesc, SortMode
 from grouped_gemm_gpu_kernel_amd.workloads import DeviceWorkload, custom_spec, make_spec
 from oracle import oracle as O
+from schedule_plan import plan_schedule
 
 pytestmark = pytest.mark.gpu
 
@@ -219,6 +220,42 @@ def test_grid_size_and_occupancy(torch):
                     c2 = KernelConfig.named(config, use_tensor_cores=mfma, persistent_ctas=persistent)
                     assert api.grid_ctas_for(c2, total) == O.grid_ctas(total, persistent, info.sm_count,
                                                                        info.active_blocks_per_sm)
+
+
+@pytest.mark.parametrize("config", CONFIGS)
+@pytest.mark.parametrize("count", [30, 700])
+def test_host_schedule_is_the_longest_first_plan(torch, config, count):
+    """build()'s work-tile schedule (scheduling order, work-tile offsets in that order, chunk
+    bounds) equals the longest-first plan restated in schedule_plan.py, with zero-tile problems,
+    C on some problems only, and both the small-set and the large work tiles."""
+    rng = np.random.default_rng(count)
+    buf = torch.zeros(64, dtype=torch.float32, device="cuda")
+    ptr = buf.data_ptr()
+    problems = []
+    for i in range(count):
+        m, n, k = (int(x) for x in np.exp(rng.uniform(0, np.log(1500), 3)).astype(int))
+        if rng.random() < 0.1:
+            m = 0
+        with_c = bool(rng.random() < 0.5)
+        problems.append(ProblemDesc(m, n, k, ptr, ptr, ptr if with_c else None, ptr, max(1, k), max(1, n),
+                                    max(1, n), max(1, n), 1.0, 0.5 if with_c else 0.0))
+    cfg = KernelConfig.named(config)
+    for mode in SortMode:
+        prep = api.prepare_problem_set(problems, cfg, mode)
+        ex = GroupedGemmExecutor()
+        assert ex.build(prep, cfg) == 0
+        shape, order, offsets, bounds = ex.schedule()
+        work = []
+        for p in prep.sorted_problems:
+            tm = -(-p.m // cfg.cta_m) if p.m > 0 and p.n > 0 else 0
+            tn = -(-p.n // cfg.cta_n) if p.m > 0 and p.n > 0 else 0
+            work.append((-(-tm // shape.tiles_m)) * (-(-tn // shape.tiles_n)))
+        want = plan_schedule([(p.m, p.n, p.k) for p in prep.sorted_problems], work, cfg.cta_m * shape.tiles_m,
+                             cfg.cta_n * shape.tiles_n, shape.stage_k,
+                             [p.c is not None and p.beta != 0.0 for p in prep.sorted_problems])
+        say(f"{config} {count} {mode.name}: work shape {shape.tiles_m}x{shape.tiles_n}, {offsets[-1]} work tiles")
+        assert (order, offsets, bounds) == want, (config, count, mode)
+        ex.close()
 
 
 def test_error_behaviour(torch):

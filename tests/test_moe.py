@@ -3,7 +3,7 @@
 The prepared set it writes on the GPU must equal, bit for bit, what the host path gives for the same
 problems: prepare_problem_set's permutation and tile offsets (src/grouped_gemm.cu:967-1022, itself
 pinned to the oracle and the reference's published rows), the descriptors build() uploads, and the
-schedule build() plans (longest processing time first, restated below in _plan_schedule).  D must equal the host path's D bit for bit (same kernel, same tiles) and the
+schedule build() plans (longest processing time first, restated in schedule_plan.py).  D must equal the host path's D bit for bit (same kernel, same tiles) and the
 oracle's host GEMM within 1e-3*sqrt(K)*max|A|*max|B|*|alpha| + 1e-6*(|beta|*max|C| + 1).  Counts are
 untrusted input: negative or oversubscribed counts are clamped and reported, never read or written
 out of bounds.  Runs are captured in a graph and replayed with new counts."""
@@ -19,6 +19,7 @@ import torch
 from grouped_gemm_gpu_kernel_amd import _lib, api, torch_ops
 from grouped_gemm_gpu_kernel_amd.api import KernelConfig, ProblemDesc, SortMode
 from oracle import oracle as O
+from schedule_plan import plan_schedule
 
 
 def test_moe_symbols_and_layout_struct(tmp_path):
@@ -114,44 +115,6 @@ def _read_device_set(plan, experts):
     return descs, offs, perm, order, head
 
 
-def _plan_schedule(shapes, work, bm, bn, bk, reads_c):
-    """The host build's schedule (plan_schedule, csrc/grouped_gemm.cpp) for problems in sorted order:
-    shapes[i] = (m, n, k), work[i] work tiles of bm x bn.  Estimated time of a problem in hundredths
-    of a cycle: sum over its tm x tn work tiles of 150 + stages (31 + 0.029 (rows + cols)) +
-    0.0023 rows cols (x2 with C), i.e. 1500000 W + stages (310000 W + 290 (m tn + n tm)) + 23 m n (46
-    with C), each operation rounded in double, then taken as an integer clamped to 2^52.  Problems go
-    whole, longest first (stable), to the first least-loaded of the 8 chunks (integer loads); within
-    a chunk, longest work tile (unclamped time / W) first, then position.
-    Returns (order, work offsets in that order, chunk bounds)."""
-    count = len(shapes)
-    total, key = [0] * count, [0.0] * count
-    for i, ((m, n, k), w) in enumerate(zip(shapes, work)):
-        if w <= 0:
-            continue
-        tm, tn = (m - 1) // bm + 1, (n - 1) // bn + 1
-        wt = float(tm) * tn
-        stages = float((k - 1) // bk + 1) if k > 0 else 0.0
-        edge = float(m) * tn + float(n) * tm
-        stage = 310000.0 * wt + 290.0 * edge
-        area = float(m) * n
-        t = 1500000.0 * wt + stages * stage + (46.0 if reads_c else 23.0) * area
-        total[i] = int(t) if t < 2.0 ** 52 else 1 << 52
-        key[i] = t / w
-    chunks = _lib.GGK_SCHEDULER_CHUNKS
-    load = [0] * chunks
-    members = [[] for _ in range(chunks)]
-    for i in sorted(range(count), key=lambda i: -total[i]):
-        c = min(range(chunks), key=lambda d: load[d])  # the first least-loaded chunk
-        load[c] += total[i]
-        members[c].append(i)
-    order, offsets, bounds = [], [0], [0]
-    for c in range(chunks):
-        for i in sorted(members[c], key=lambda i: (-key[i], i)):
-            order.append(i)
-            offsets.append(offsets[-1] + work[i])
-        bounds.append(offsets[-1])
-    return order, offsets, bounds
-
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("config", ["64x64x16", "128x64x32", "64x128x32"])
@@ -184,7 +147,7 @@ def test_device_prepare_equals_host_prepare(torch_cuda, config, experts):
             want = (p.m, p.n, p.k, p.a, p.b, p.c or 0, p.d, p.lda, p.ldb, p.ldc, p.ldd, p.alpha, p.beta, tm, tn)
             assert got == want, (config, experts, mode, i)
             work.append((-(-tm // shape.tiles_m)) * (-(-tn // shape.tiles_n)))
-        want_order, want_offsets, want_bounds = _plan_schedule(
+        want_order, want_offsets, want_bounds = plan_schedule(
             [(p.m, p.n, p.k) for p in prep.sorted_problems], work, cfg.cta_m * shape.tiles_m,
             cfg.cta_n * shape.tiles_n, shape.stage_k, True)
         assert sorted(want_order) == list(range(experts))

@@ -55,6 +55,9 @@ struct GroupedArgs {
   const int* __restrict__ work_offsets;  // work tiles, in scheduling order: [count + 1]
   // Problem at each scheduling position (NULL: position = problem index).
   const int* __restrict__ order;
+  // (problem, work tile within it) of each work-tile index: [2 * total]
+  // (NULL: found from work_offsets and order).
+  const int* __restrict__ work_table;
   int count;
   int total;           // work tiles
   int* state;          // chunk c's claim counter at [c * kStride], retired workgroups at [kChunks * kStride]
@@ -248,11 +251,18 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       return true;
     };
 
-    const int pos = find_problem(args.work_offsets, args.count, t);
-    const int prob = args.order != nullptr ? ((const_int_ptr)args.order)[pos] : pos;
+    int prob, local;
+    if (args.work_table != nullptr) {
+      // One scalar load instead of the search's chain of dependent ones.
+      prob = ((const_int_ptr)args.work_table)[2 * t];
+      local = ((const_int_ptr)args.work_table)[2 * t + 1];
+    } else {
+      const int pos = find_problem(args.work_offsets, args.count, t);
+      prob = args.order != nullptr ? ((const_int_ptr)args.order)[pos] : pos;
+      local = t - ((const_int_ptr)args.work_offsets)[pos];
+    }
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
     const gg_device_problem_desc p = load_problem(args.problems, prob);
-    const int local = t - ((const_int_ptr)args.work_offsets)[pos];
     const int wtn = work_tiles_n<S::TM, S::TN>(p);
     if (wtn > 0) {
       const int wm = local / wtn;
@@ -517,9 +527,9 @@ static bool bounds_valid(const int* chunk_bounds, int total) {
 
 static hipError_t launch_grouped(int variant, int path, int addressing, bool traced,
                                  const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
-                                 const int* d_work_offsets, const int* d_order, int problem_count,
-                                 int total_work, int* d_state, const int* chunk_bounds, int grid, int* d_tile_map,
-                                 long long* d_wg_clock, hipStream_t stream) {
+                                 const int* d_work_offsets, const int* d_order, const int* d_work_table,
+                                 int problem_count, int total_work, int* d_state, const int* chunk_bounds, int grid,
+                                 int* d_tile_map, long long* d_wg_clock, hipStream_t stream) {
   if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_work < 0 ||
       (addressing != GGK_ADDR_32 && addressing != GGK_ADDR_64)) {
     return hipErrorInvalidValue;
@@ -530,8 +540,8 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
   }
   if (traced && d_tile_map != nullptr && d_tile_offsets == nullptr) return hipErrorInvalidDevicePointer;
   if (!bounds_valid(chunk_bounds, total_work)) return hipErrorInvalidValue;
-  GroupedArgs args{d_problems, d_tile_offsets, d_work_offsets, d_order, problem_count, total_work, d_state,
-                   traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}, nullptr};
+  GroupedArgs args{d_problems, d_tile_offsets, d_work_offsets, d_order, d_work_table, problem_count, total_work,
+                   d_state, traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}, nullptr};
   fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];
@@ -572,10 +582,11 @@ int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* proble
 }
 
 hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
-                              const int* d_work_offsets, const int* d_order, int problem_count, int total_work,
-                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream) {
-  return launch_grouped(variant, path, addressing, false, d_problems, nullptr, d_work_offsets, d_order, problem_count,
-                        total_work, d_state, chunk_bounds, grid, nullptr, nullptr, stream);
+                              const int* d_work_offsets, const int* d_order, const int* d_work_table,
+                              int problem_count, int total_work, int* d_state, const int* chunk_bounds, int grid,
+                              hipStream_t stream) {
+  return launch_grouped(variant, path, addressing, false, d_problems, nullptr, d_work_offsets, d_order, d_work_table,
+                        problem_count, total_work, d_state, chunk_bounds, grid, nullptr, nullptr, stream);
 }
 
 hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
@@ -589,8 +600,8 @@ hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, cons
   if (d_problems == nullptr || d_work_offsets == nullptr || d_state == nullptr || d_header == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
-  GroupedArgs args{d_problems, nullptr, d_work_offsets, d_order, problem_count, 0, d_state, nullptr, nullptr, {},
-                   d_header};
+  GroupedArgs args{d_problems, nullptr, d_work_offsets, d_order, nullptr, problem_count, 0, d_state, nullptr, nullptr,
+                   {}, d_header};
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];
   return hipLaunchKernel(reinterpret_cast<const void*>(k.grouped[addressing]), dim3(grid), dim3(k.threads), params,
@@ -599,11 +610,12 @@ hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, cons
 
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
-                                     const int* d_work_offsets, const int* d_order, int problem_count,
-                                     int total_work, int* d_state, const int* chunk_bounds, int grid,
-                                     int* d_tile_map, long long* d_wg_clock, hipStream_t stream) {
+                                     const int* d_work_offsets, const int* d_order, const int* d_work_table,
+                                     int problem_count, int total_work, int* d_state, const int* chunk_bounds,
+                                     int grid, int* d_tile_map, long long* d_wg_clock, hipStream_t stream) {
   return launch_grouped(variant, path, addressing, true, d_problems, d_tile_offsets, d_work_offsets, d_order,
-                        problem_count, total_work, d_state, chunk_bounds, grid, d_tile_map, d_wg_clock, stream);
+                        d_work_table, problem_count, total_work, d_state, chunk_bounds, grid, d_tile_map, d_wg_clock,
+                        stream);
 }
 
 hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,

@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <array>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <numeric>
 #include <tuple>
@@ -355,7 +356,8 @@ struct GroupedGemmExecutor::Impl {
   DeviceProblemDesc* d_problems = nullptr;
   int* d_tile_offsets = nullptr;  // [problem_count + 1] reference tile offsets, then
                                   // [problem_count + 1] work-tile offsets in scheduling
-                                  // order, then [problem_count] the scheduling order
+                                  // order, then [problem_count] the scheduling order,
+                                  // then (if work_table) [2 * total_work] the work table
   int* d_state = nullptr;
 
   int problem_count = 0;
@@ -368,7 +370,25 @@ struct GroupedGemmExecutor::Impl {
   int path = GGK_PATH_FMA;
   int addressing = GGK_ADDR_32;
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> chunk_bounds{};
+  bool work_table = false;
+
+  const int* d_work_table() const {
+    return work_table ? d_tile_offsets + 3 * static_cast<size_t>(problem_count) + 2 : nullptr;
+  }
 };
+
+namespace {
+
+// Work tables up to this many work tiles (8 bytes each) are uploaded; larger
+// sets, and every set when the environment sets GG_WORK_TABLE=0, are searched.
+constexpr int kWorkTableMax = 1 << 22;
+
+bool work_table_enabled() {
+  const char* v = std::getenv("GG_WORK_TABLE");
+  return v == nullptr || std::strcmp(v, "0") != 0;
+}
+
+}  // namespace
 
 GroupedGemmExecutor::GroupedGemmExecutor() : impl_(new Impl()) {}
 
@@ -472,6 +492,18 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   std::vector<int> offsets(prepared.tile_offsets);
   offsets.insert(offsets.end(), schedule.work_offsets.begin(), schedule.work_offsets.end());
   offsets.insert(offsets.end(), schedule.order.begin(), schedule.order.end());
+  // The work table: (problem, work tile within it) of every work-tile index,
+  // so that the kernel reads it with one load instead of searching.
+  impl_->work_table = impl_->total_work > 0 && impl_->total_work <= kWorkTableMax && work_table_enabled();
+  if (impl_->work_table) {
+    offsets.reserve(offsets.size() + 2 * static_cast<size_t>(impl_->total_work));
+    for (const int prob : schedule.order) {
+      for (int w = 0; w < work[prob]; ++w) {
+        offsets.push_back(prob);
+        offsets.push_back(w);
+      }
+    }
+  }
 
   if (problem_count > 0) {
     status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems),
@@ -509,9 +541,9 @@ hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
                             impl_->d_tile_offsets + impl_->problem_count + 1,
-                            impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->problem_count,
-                            impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(), impl_->grid_ctas,
-                            stream);
+                            impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
+                            impl_->problem_count, impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(),
+                            impl_->grid_ctas, stream);
 }
 
 hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
@@ -519,9 +551,9 @@ hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_cloc
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
   return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
                                    impl_->d_tile_offsets, impl_->d_tile_offsets + impl_->problem_count + 1,
-                                   impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->problem_count,
-                                   impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(),
-                                   impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
+                                   impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
+                                   impl_->problem_count, impl_->total_work, impl_->d_state,
+                                   impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
 }
 
 int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }

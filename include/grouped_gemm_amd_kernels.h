@@ -174,10 +174,15 @@ int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* proble
  * GGK_SCHEDULER_STATE_INTS zeroed ints.  chunk_bounds (host memory,
  * GGK_SCHEDULER_CHUNKS + 1 non-decreasing ints from 0 to total_work, or NULL
  * for equal counts) splits the work-tile indices into the per-XCD chunks.
- * grid workgroups claim work tiles until total_work are done. */
+ * d_work_table[2 * total_work] (device memory, or NULL) holds for each
+ * work-tile index the problem (in sorted order) and the work tile's index
+ * within that problem (row-major), which the kernel then reads instead of
+ * searching d_work_offsets for them.  grid workgroups claim work tiles until
+ * total_work are done. */
 hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
-                              const int* d_work_offsets, const int* d_order, int problem_count, int total_work,
-                              int* d_state, const int* chunk_bounds, int grid, hipStream_t stream);
+                              const int* d_work_offsets, const int* d_order, const int* d_work_table,
+                              int problem_count, int total_work, int* d_state, const int* chunk_bounds, int grid,
+                              hipStream_t stream);
 
 /* The same scheduler with instrumentation.  d_tile_map (may be NULL; needs
  * d_tile_offsets, the reference tile offsets of the problems in sorted
@@ -188,9 +193,9 @@ hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_de
  * the GEMM is computed as usual. */
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
-                                     const int* d_work_offsets, const int* d_order, int problem_count,
-                                     int total_work, int* d_state, const int* chunk_bounds, int grid,
-                                     int* d_tile_map, long long* d_wg_clock, hipStream_t stream);
+                                     const int* d_work_offsets, const int* d_order, const int* d_work_table,
+                                     int problem_count, int total_work, int* d_state, const int* chunk_bounds,
+                                     int grid, int* d_tile_map, long long* d_wg_clock, hipStream_t stream);
 
 /* Device-resident preparation of a mixture-of-experts group (no reference
  * counterpart: it is the step before the grouped launch in MoE use, done here

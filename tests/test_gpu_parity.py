@@ -168,15 +168,19 @@ def _mapping_sets():
 
 
 @pytest.mark.parametrize("config", CONFIGS)
-def test_tile_mapping_bit_exact(torch, config):
+@pytest.mark.parametrize("work_table", [True, False])
+def test_tile_mapping_bit_exact(torch, config, work_table, monkeypatch):
     """The scheduler's tile -> (problem, tile_m, tile_n) function equals find_problem_by_tile plus the
-    row-major local tile (src/grouped_gemm.cu:219-234, 659-668), for every claimed index."""
+    row-major local tile (src/grouped_gemm.cu:219-234, 659-668), for every claimed index: read from
+    the executor's work table, and found by the kernel's own search (GG_WORK_TABLE=0 at build)."""
+    if not work_table:
+        monkeypatch.setenv("GG_WORK_TABLE", "0")
     cfg = KernelConfig.named(config)
     for name, shapes in _mapping_sets().items():
         shapes = [(int(a), int(b), int(c)) for a, b, c in shapes]
         buf, probs = _dummy_problems(torch, shapes)
         for mode in (SortMode.kNone, SortMode.kByK, SortMode.kByTiles):
-            say(f"mapping {config} {name} mode={int(mode)}")
+            say(f"mapping {config} {name} mode={int(mode)} work_table={work_table}")
             prep = api.prepare_problem_set(probs, cfg, mode)
             ex = GroupedGemmExecutor()
             assert ex.build(prep, cfg) == 0

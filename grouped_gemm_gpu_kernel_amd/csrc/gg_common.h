@@ -167,7 +167,11 @@ template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   static constexpr int STAGE_BYTES = 2 * GG_STAGE_K * (BM + BN);
   static constexpr int BUFFERS =
       GG_DMA_BUFFERS > 0 ? GG_DMA_BUFFERS : (THREADS >= 512 && 3 * STAGE_BYTES <= 150 * 1024 ? 3 : 2);
-  using G = Geometry<BM, BN, GG_STAGE_K, GG_STAGE_DEPTH, THREADS, BUFFERS, true>;
+  // Register staging serves only the 64-bit addressing form here; a ring of
+  // two stages keeps it within the registers beside the accumulators (the
+  // 256 x 256 work tile's still spills: launches route that form to the
+  // 128 x 128 work tile of the same macro-tile).
+  using G = Geometry<BM, BN, GG_STAGE_K, 2, THREADS, BUFFERS, true>;
 };
 template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr int TM = 1;
@@ -684,9 +688,12 @@ __device__ __forceinline__ void stage_barrier() {
 }
 
 // D = alpha * acc + beta * C for one element; C is read only when c != nullptr
-// and beta != 0 (src/grouped_gemm.cu:475-479, 616-621).
+// and beta != 0 (src/grouped_gemm.cu:475-479, 616-621).  One fixed rounding
+// sequence -- beta * C rounded, then one fused multiply-add -- so that every
+// work-tile shape, addressing form and path gives the same bits (left to the
+// compiler, the contraction differs between code shapes).
 __device__ __forceinline__ float epilogue_value(float acc, float c, float alpha, float beta) {
-  return alpha * acc + beta * c;
+  return __builtin_fmaf(alpha, acc, beta * c);
 }
 
 }  // namespace gg

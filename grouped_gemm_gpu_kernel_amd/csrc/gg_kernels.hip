@@ -621,6 +621,11 @@ hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
 hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,
                              hipStream_t stream) {
   if (!valid_kernel(variant, path) || problem == nullptr) return hipErrorInvalidValue;
+  // The 64-bit form of the 256 x 256 work tile spills registers: such a
+  // problem runs on 128 x 128 work tiles of the same macro-tile (same D).
+  if (path == GGK_PATH_MFMA && variant == GGK_VARIANT_128x64x32 && !fits_addr32(kKernels[variant][path], *problem)) {
+    variant = GGK_VARIANT_128x64x32_SMALL;
+  }
   const KernelSet& k = kKernels[variant][path];
   if (problem->tiles_m <= 0 || problem->tiles_n <= 0) return hipSuccess;
   const int64_t work = (int64_t)((problem->tiles_m + k.tm - 1) / k.tm) * ((problem->tiles_n + k.tn - 1) / k.tn);

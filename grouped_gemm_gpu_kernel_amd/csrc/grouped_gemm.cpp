@@ -478,10 +478,25 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
       return hipErrorInvalidValue;
     }
-    // Never above the problem's tile count, so the sums fit an int.
-    work[i] = ceil_div(dp.tiles_m, mode.work.tiles_m) * ceil_div(dp.tiles_n, mode.work.tiles_n);
     if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
     device_problems.push_back(dp);
+  }
+  // The 64-bit form of the 256 x 256 work tile spills registers: a set that
+  // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
+  if (impl_->addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
+    mode.variant = GGK_VARIANT_128x64x32_SMALL;
+    status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
+    if (status != hipSuccess) return status;
+    impl_->variant = mode.variant;
+    impl_->addressing = GGK_ADDR_32;
+    for (const DeviceProblemDesc& dp : device_problems) {
+      if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
+    }
+  }
+  for (int i = 0; i < problem_count; ++i) {
+    // Never above the problem's tile count, so the sums fit an int.
+    const DeviceProblemDesc& dp = device_problems[i];
+    work[i] = ceil_div(dp.tiles_m, mode.work.tiles_m) * ceil_div(dp.tiles_n, mode.work.tiles_n);
   }
   const Schedule schedule = plan_schedule(device_problems, work, config.cta_m * mode.work.tiles_m,
                                           config.cta_n * mode.work.tiles_n, mode.work.stage_k);
@@ -719,8 +734,15 @@ hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& co
   probe.beta = L.beta;
   probe.tiles_m = 1;
   probe.tiles_n = 1;
-  const int wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
+  int wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   if (wide < 0) return hipErrorInvalidValue;
+  // As in GroupedGemmExecutor::build: no 64-bit 256 x 256 work tiles.
+  if (wide == 1 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
+    mode.variant = GGK_VARIANT_128x64x32_SMALL;
+    status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
+    if (status != hipSuccess) return status;
+    wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
+  }
 
   release(impl_->d_problems, impl_->d_ints, impl_->d_state);
   const size_t ints = 2 * static_cast<size_t>(e + 1) + 2 * static_cast<size_t>(e) + GGK_MOE_HEADER_INTS;

@@ -433,6 +433,54 @@ def test_wide_leading_dimensions(torch):
                         f"{config} mfma={mfma} {run} {(m, n, k)}"
 
 
+def test_wide_set_runs_on_128x128_work_tiles(torch):
+    """A 128x64x32 set large enough for 256 x 256 work tiles, plus one problem whose leading dimension
+    needs 64-bit addressing, runs on 128 x 128 work tiles (the 64-bit 256 x 256 form would spill
+    registers): the other problems' D is bit-identical to the same set without the wide problem (256 x
+    256 tiles, 32-bit form), and the wide problem's D is within the oracle bound; the per-problem
+    baseline routes the wide problem the same way."""
+    cfg = KernelConfig.named("128x64x32")
+    count, m, n, k = 1100, 128, 128, 16
+    g = torch.Generator(device="cpu").manual_seed(21)
+    a = (torch.rand(m, k, generator=g) * 2 - 1).half().cuda()
+    b = (torch.rand(k, n, generator=g) * 2 - 1).half().cuda()
+    c = (torch.rand(m, n, generator=g) * 2 - 1).cuda()
+    d = torch.full((count, m, n), float("nan"), device="cuda")
+    fill = [ProblemDesc(m, n, k, a.data_ptr(), b.data_ptr(), c.data_ptr(), d[i].data_ptr(), k, n, n, n, 1.25, 0.5)
+            for i in range(count)]
+    wm, wn, wk, wide_lda = 70, 90, 33, (1 << 24) + 3
+    wa = torch.empty((wm - 1) * wide_lda + wk, dtype=torch.float16, device="cuda").uniform_(-1, 1)
+    wb = (torch.rand(wk, wn, generator=g) * 2 - 1).half().cuda()
+    wd = torch.full((wm, wn), float("nan"), device="cuda")
+    wide = ProblemDesc(wm, wn, wk, wa.data_ptr(), wb.data_ptr(), None, wd.data_ptr(), wide_lda, wn, wn, wn, 1.5, 0.0)
+    ah = torch.as_strided(wa, (wm, wk), (wide_lda, 1)).cpu().numpy().view(np.uint16).reshape(-1).copy()
+    want_wide = O.gemm(wm, wn, wk, ah, wk, wb.cpu().numpy().view(np.uint16).reshape(-1), wn, None, wn, 1.5, 0.0)
+
+    ex = GroupedGemmExecutor()
+    assert ex.build(api.prepare_problem_set(fill, cfg, SortMode.kByTiles), cfg) == 0
+    assert ex.schedule()[0].tiles_m == 2  # 256 x 256 work tiles
+    assert ex.run() == 0
+    torch.cuda.synchronize()
+    d_large = d.clone()
+    ex.close()
+    d.fill_(float("nan"))
+    ex = GroupedGemmExecutor()
+    assert ex.build(api.prepare_problem_set(fill + [wide], cfg, SortMode.kByTiles), cfg) == 0
+    shape = ex.schedule()[0]
+    say(f"wide set: work shape {shape.tiles_m}x{shape.tiles_n}")
+    assert (shape.tiles_m, shape.tiles_n) == (1, 2)  # 128 x 128 work tiles
+    assert ex.run() == 0
+    torch.cuda.synchronize()
+    assert torch.equal(d, d_large)
+    got = wd.cpu().numpy().reshape(-1)
+    assert np.abs(got - want_wide).max() <= tolerance(wk, 1.0, 1.0, 0.0, 1.5, 0.0)
+    ex.close()
+    wd.fill_(float("nan"))
+    assert api.run_baseline_per_problem([wide], cfg) == 0
+    torch.cuda.synchronize()
+    assert np.abs(wd.cpu().numpy().reshape(-1) - want_wide).max() <= tolerance(wk, 1.0, 1.0, 0.0, 1.5, 0.0)
+
+
 def test_persistent_grid_sizes_and_repeated_runs(torch):
     """Any persistent grid gives bit-identical D; runs of one executor back to back (the scheduler state
     returns to zero by itself) stay identical."""

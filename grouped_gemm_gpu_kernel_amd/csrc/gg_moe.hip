@@ -64,6 +64,19 @@ __device__ double problem_work_time(int m, int n, int k, int tm, int tn, int bk,
 // 64 bits (below 2^53 the double is an exact integer already).
 __device__ long long problem_time_units(double t) { return t < 4503599627370496.0 ? (long long)t : (1LL << 52); }
 
+// Lane i takes lane i + SH's (value, index) pair when it is the lesser one
+// (row shift within 16 lanes; the lanes it leaves undefined are not used).
+template <int SH>
+__device__ __forceinline__ void least_from(unsigned long long& v, int& idx) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x100 + SH, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x100 + SH, 0xf, 0xf, false);
+  const int pidx = __builtin_amdgcn_update_dpp(0, idx, 0x100 + SH, 0xf, 0xf, false);
+  const unsigned long long pv = ((unsigned long long)hi << 32) | lo;
+  const bool take = pv < v || (pv == v && pidx < idx);
+  v = take ? pv : v;
+  idx = take ? pidx : idx;
+}
+
 // Exclusive prefix sum of one value per thread over the workgroup, in thread
 // order; *total receives the sum.  Every thread must call it.
 template <class T>
@@ -245,34 +258,32 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   __syncthreads();
   if (tid < kWave) {
     // Greedy assignment by wave 0, one position at a time onto the first
-    // least-loaded chunk.  The loads are exact integers, uniform across the
-    // wave (scalar registers); the estimated times come from LDS 64 at a
-    // time, one per lane, and each step takes its own from its lane.
+    // least-loaded chunk.  Lane c < kChunks holds chunk c's load (an exact
+    // integer), the other lanes a load no chunk reaches; the least (load,
+    // lane) pair reaches lane 0 in three row shifts, so ties go to the lower
+    // chunk as in a scan.  The estimated times come from LDS 64 at a time, one
+    // per lane; each step takes its own from its lane and leaves its choice
+    // in that lane.
     const int lane = tid;
-    long long load[kChunks];
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) load[c] = 0;
+    unsigned long long load = lane < kChunks ? 0ull : ~0ull;
     for (int r0 = 0; r0 < experts; r0 += kWave) {
       const int r = r0 + lane;
-      const long long mine = r < experts ? s_by_total[r] : 0;
-      const int lo = (int)(unsigned long long)mine;
-      const int hi = (int)((unsigned long long)mine >> 32);
+      const unsigned long long mine = r < experts ? (unsigned long long)s_by_total[r] : 0ull;
+      const int mine_lo = (int)(uint32_t)mine;
+      const int mine_hi = (int)(uint32_t)(mine >> 32);
       const int steps = min(kWave, experts - r0);
       int chosen = 0;  // lane j: the chunk of by-total rank r0 + j
       for (int j = 0; j < steps; ++j) {
-        const long long t = (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane(hi, j) << 32) |
-                                        (unsigned)__builtin_amdgcn_readlane(lo, j));
-        int best = 0;
-        long long least = load[0];
-#pragma unroll
-        for (int c = 1; c < kChunks; ++c) {
-          if (load[c] < least) {  // strict: ties stay with the lower chunk
-            least = load[c];
-            best = c;
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c) load[c] = c == best ? load[c] + t : load[c];
+        const unsigned long long t =
+            ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane(mine_hi, j) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane(mine_lo, j);
+        unsigned long long v = load;
+        int idx = lane;
+        least_from<4>(v, idx);
+        least_from<2>(v, idx);
+        least_from<1>(v, idx);
+        const int best = __builtin_amdgcn_readfirstlane(idx);
+        load = lane == best ? load + t : load;
         chosen = lane == j ? best : chosen;
       }
       if (r < experts) s_chunk[s_order[r]] = chosen;

@@ -41,6 +41,8 @@ def parse_args():
     ap.add_argument("--no-torch-op", action="store_true", help="skip the torch binding timings")
     ap.add_argument("--no-vendor", action="store_true", help="skip the hipBLASLt comparison rows")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="time the CPU baseline over the whole workload (minutes on mixed-512) instead of samples")
     ap.add_argument("--fma", action="store_true", help="FMA tile path instead of MFMA")
     ap.add_argument("--table", action="store_true", help="also print the reference-style results table")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -82,6 +84,29 @@ def time_runs(torch, fn, steps: int, warmup: int) -> float:
     stop.synchronize()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def timed_prepare_and_build(probs, cfg, mode):
+    """(executor, ms) for prepare_problem_set + build through the C-ABI, timed on the host."""
+    import ctypes
+
+    from grouped_gemm_gpu_kernel_amd import _lib, api
+
+    count = len(probs)
+    arr = api._problem_array(probs)
+    cfg_c = cfg.to_c()
+    out = (_lib.GGProblemDesc * max(1, count))()
+    perm = (ctypes.c_int * max(1, count))()
+    offs = (ctypes.c_int * (count + 1))()
+    ex = api.GroupedGemmExecutor()
+    L = _lib.lib()
+    t0 = time.perf_counter()
+    total = L.gg_prepare_problem_set(arr, count, ctypes.byref(cfg_c), int(mode), out, perm, offs)
+    st = L.gg_executor_build(ex._handle, out, count, offs, count + 1, total, ctypes.byref(cfg_c))
+    ms = (time.perf_counter() - t0) * 1e3
+    if total < 0 or st != 0:
+        raise RuntimeError(f"prepare/build failed: total {total}, hipError_t {st}")
+    return ex, ms
 
 
 def measured_tail_idle(torch, ex) -> float:
@@ -137,7 +162,10 @@ def moe_device_prepare(torch, dw, spec, cfg, mode, stream, steps: int, warmup: i
     a_pool = dw.a.view(torch.float16)
     b_pool = dw.b.view(torch.float16)
     a = torch.cat([a_pool[int(o):int(o) + int(m) * k].view(int(m), k) for o, m in zip(dw.a_off, rows)])
-    b = torch.stack([b_pool[int(o):int(o) + k * n].view(k, n) for o in dw.b_off])
+    if all(int(o) == i * k * n for i, o in enumerate(dw.b_off)):
+        b = b_pool[:spec.count * k * n].view(spec.count, k, n)  # the pool already is [E, K, N]
+    else:
+        b = torch.stack([b_pool[int(o):int(o) + k * n].view(k, n) for o in dw.b_off])
     d = torch.empty(int(rows.sum()), n, dtype=torch.float32, device=a.device)
     counts = torch.from_numpy(rows.astype(np.int32)).cuda()
     plan = torch_ops.MoeGroupedGemmPlan(a, b, d, None, float(spec.alpha[0]), float(spec.beta[0]), sort_mode=mode,
@@ -166,37 +194,89 @@ def vendor_baseline(spec, config_name: str, sort_mode: int, steps: int, warmup: 
     return res
 
 
-def cpu_baseline(dw, spec, seconds: float):
-    """The oracle's FP32 host GEMM (OpenMP form of the reference's loop, bit-identical to it) on a
-    bounded prefix of the same problems, on this host's cores."""
-    import numpy as np
+def host_cpu_info() -> dict:
+    """The host the CPU baseline ran on: CPU model, logical CPUs, the CPUs this process may use and
+    the OpenMP thread setting."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
+
+def cpu_gemm_sample(dw, spec, seconds: float, threads, full: bool = False) -> dict:
+    """The oracle's host GEMM (tests/test_correctness.cu:85-102) over the workload's problems in index
+    order until `seconds` have passed: threads=None runs the literal single-thread i-j-k loop, an int
+    the OpenMP i-k-j form on that many threads (bit-identical per element).  Each call computes a
+    block of rows of one problem (full=True: every row of every problem, no time limit), so one large
+    problem cannot overrun the budget; rows give the same per-element arithmetic as the whole."""
     from oracle import oracle as O
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    done_flops, elapsed, used = 0.0, 0.0, 0
-    order = list(range(spec.count))
-    for i in order:
+    done_flops, elapsed, problems, rows_done = 0.0, 0.0, 0, 0
+    for i in range(spec.count):
         m, n, k = int(spec.m[i]), int(spec.n[i]), int(spec.k[i])
         if m <= 0 or n <= 0:
             continue
-        a, b, c = dw.host_a(i), dw.host_b(i), dw.host_c(i)
+        per_row = 2.0 * n * k
+        # about 5e7 flops per call single-threaded, `threads` times that in parallel
+        rows = m if full else max(1, min(m, int(5e7 * (threads or 1) / max(per_row, 1.0)) + 1))
+        a = dw.host_a(i)[:rows * max(1, k)]
+        b = dw.host_b(i)
+        c = dw.host_c(i)
+        c = c[:rows * n] if c is not None else None
         t0 = time.perf_counter()
-        O.gemm(m, n, k, a, max(1, k), b, max(1, n), c, max(1, n), float(spec.alpha[i]), float(spec.beta[i]),
+        O.gemm(rows, n, k, a, max(1, k), b, max(1, n), c, max(1, n), float(spec.alpha[i]), float(spec.beta[i]),
                threads=threads)
         elapsed += time.perf_counter() - t0
-        done_flops += 2.0 * m * n * k
-        used += 1
-        if elapsed >= seconds:
+        done_flops += per_row * rows
+        problems += 1
+        rows_done += rows
+        if not full and elapsed >= seconds:
             break
-    return {
-        "value": round(done_flops / elapsed / 1e12, 6) if elapsed > 0 else None,
+    return {"tflops": done_flops / elapsed / 1e12 if elapsed > 0 else None, "gflop": round(done_flops / 1e9, 3),
+            "seconds": round(elapsed, 2), "problems": problems, "rows": rows_done}
+
+
+def cpu_baseline(dw, spec, seconds: float, full: bool = False):
+    """CPU baseline on this host's cores: the OpenMP form on every thread OpenMP is given
+    (OMP_NUM_THREADS, else every CPU this process may use) is `value`; the literal single-thread loop
+    rides along, timed on the 16-problem plumbing set in full and on a sample of this workload.
+    full=True times the whole workload in both forms instead of samples."""
+    from grouped_gemm_gpu_kernel_amd.workloads import DeviceWorkload, make_spec
+
+    info = host_cpu_info()
+    threads = int(info["omp_num_threads"] or info["affinity_cpus"])
+    omp = cpu_gemm_sample(dw, spec, seconds / 2, threads, full)
+    single = cpu_gemm_sample(dw, spec, seconds / 2, None, full)
+    plumbing_spec = make_spec("plumbing16")
+    plumbing = cpu_gemm_sample(DeviceWorkload(plumbing_spec), plumbing_spec, 0.0, None, True)
+
+    def what(r):
+        return ("all rows of all" if full else f"row blocks of the first {r['problems']} of {spec.count}") + \
+            f" problems ({r['gflop']} GFLOP, {r['seconds']} s)"
+
+    out = {
+        "value": round(omp["tflops"], 6) if omp["tflops"] else None,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"first {used} of {spec.count} problems of the same set ({done_flops / 1e9:.1f} GFLOP, "
-                  f"{elapsed:.1f} s), oracle FP32 host GEMM, OpenMP over rows, {threads} threads",
+        "sample": f"{spec.name}: {what(omp)}; oracle FP32 host GEMM, OpenMP i-k-j form on {threads} threads",
+        "host": info,
+        "single_thread": {
+            "tflops": round(single["tflops"], 6) if single["tflops"] else None,
+            "sample": f"{spec.name}: {what(single)}; literal i-j-k loop, 1 thread"},
+        "single_thread_plumbing16": {
+            "tflops": round(plumbing["tflops"], 6) if plumbing["tflops"] else None,
+            "ms": round(plumbing["seconds"] * 1e3, 1), "gflop": plumbing["gflop"]},
     }
+    print(f"# cpu baseline {out}", file=sys.stderr, flush=True)
+    return out
 
 
 def _csv_rows(path: Path):
@@ -243,23 +323,23 @@ def profile_summary(dirs, kernel_filter: str) -> int:
     return 0
 
 
-def committed_traffic(workload: str):
-    """HBM bytes per launch of the grouped kernel on `workload`, from the committed rocprofv3 summary
-    profiles/gg_grouped_kernel_<workload>_hbm_traffic.txt (FETCH_SIZE and WRITE_SIZE per dispatch,
-    each scaled by the same counter's reading for a plain copy of known size), or None."""
+def committed_traffic(workload: str, mode: str):
+    """HBM bytes per launch of the grouped kernel on `workload` in sort mode `mode`, from the committed
+    rocprofv3 summary profiles/gg_grouped_kernel_<workload>_hbm_traffic.txt (FETCH_SIZE and WRITE_SIZE
+    per dispatch, each scaled by the same counter's reading for a plain copy of known size), or None.
+    The file holds one `traffic_bytes_per_launch <mode>: <bytes>` line per sort mode."""
     path = ROOT / "profiles" / f"gg_grouped_kernel_{workload}_hbm_traffic.txt"
     if not path.exists():
         return None
-    vals = {}
     for line in path.read_text().splitlines():
-        if ":" in line and not line.startswith("#"):
-            k, v = line.split(":", 1)
-            vals[k.strip()] = v.strip()
-    try:
-        return {"bytes": float(vals["traffic_bytes_per_launch"]), "mode": vals.get("sort_mode", ""),
-                "source": str(path.relative_to(ROOT))}
-    except (KeyError, ValueError):
-        return None
+        if line.startswith("traffic_bytes_per_launch ") and ":" in line:
+            key, value = line.split(":", 1)
+            if key.split()[1] == mode:
+                try:
+                    return {"bytes": float(value.strip()), "mode": mode, "source": str(path.relative_to(ROOT))}
+                except ValueError:
+                    return None
+    return None
 
 
 def main() -> int:
@@ -302,15 +382,16 @@ def main() -> int:
     # stretch of its own launches: the GPU lowers its clock within milliseconds of idling (a build,
     # a traced run, a host copy) and takes tens of milliseconds of load to raise it again, which
     # otherwise shows up as a 5-10% slower mode depending only on its place in the order.
+    # prep_ms is the reference benchmark's span (bench/benchmark_grouped_gemm.cu:622-632):
+    # prepare_problem_set + GroupedGemmExecutor::build, here the two C calls on a problem array
+    # converted from Python beforehand.  The first build in a process also queries the device and
+    # the kernel's occupancy once (cached afterwards); it is timed apart as first_build_ms.
+    first_build_ms = timed_prepare_and_build(probs, cfg, modes[0])[1]
     built = []
     for mode in modes:
-        t0 = time.perf_counter()
+        ex, prep_ms = timed_prepare_and_build(probs, cfg, mode)
         prep = api.prepare_problem_set(probs, cfg, mode)
-        ex = GroupedGemmExecutor()
-        st = ex.build(prep, cfg)
-        if st != 0:
-            raise RuntimeError(f"build hipError_t {st}")
-        built.append((mode, prep, ex, (time.perf_counter() - t0) * 1e3))
+        built.append((mode, prep, ex, prep_ms))
 
     def clock_warmup(ex, seconds: float) -> None:
         deadline = time.perf_counter() + seconds
@@ -354,7 +435,7 @@ def main() -> int:
                                                                             args.steps, args.warmup)
     torch_op = None if args.no_torch_op else torch_binding(torch, dw, cfg, best_mode, stream, args.steps,
                                                           args.warmup)
-    cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds, args.cpu_full)
 
     row, ms = best
     tflops = flops / (ms * 1e-3) / 1e12
@@ -363,7 +444,7 @@ def main() -> int:
     hbm_frac = achieved_gbs / HBM_PEAK_GBS
     ridge = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     bound = "hbm" if flops / algo_bytes < ridge else "mfma"
-    traffic = committed_traffic(spec.name) if not args.fma else None
+    traffic = committed_traffic(spec.name, row["mode"]) if not args.fma else None
     if bound == "hbm":
         roofline = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(hbm_frac, 4), "traffic": round(traffic["bytes"]) if traffic else None}
@@ -391,6 +472,8 @@ def main() -> int:
                    "gflop": round(flops / 1e9, 3), "algorithmic_gb": round(algo_bytes / 1e9, 4)},
         "mfma_peak_frac": round(mfma_frac, 4),
         "hbm_roofline_frac": round(hbm_frac, 4),
+        "prep_ms": row["prep_ms"],
+        "first_build_ms": round(first_build_ms, 3),
         "tail_share": row["tail_share"],
         "tail_idle_measured": row["tail_idle_measured"],
         "per_mode": per_mode,

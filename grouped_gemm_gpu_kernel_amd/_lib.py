@@ -11,7 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
-LIB_PATH = Path(os.environ.get("GG_LIBRARY") or (Path(__file__).resolve().parent / "lib" / "libgrouped_gemm_amd.so"))
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgrouped_gemm_amd.so"
 
 # hipError_t values used by the API (hip_runtime_api.h).
 HIP_SUCCESS = 0
@@ -151,6 +151,11 @@ SIGNATURES = {
     "ggk_zero": (_i, [_vp, ctypes.c_size_t]),
     "ggk_stream_synchronize": (_i, [_vp]),
     "ggk_device_synchronize": (_i, []),
+    "ggk_event_create": (_i, [_P(_vp)]),
+    "ggk_event_destroy": (_i, [_vp]),
+    "ggk_event_record_launch": (_i, [_vp, _vp, c_int_p]),
+    "ggk_event_synchronize": (_i, [_vp]),
+    "ggk_current_device": (_i, [c_int_p]),
     "ggk_device_info_get": (_i, [_P(GGKDeviceInfo)]),
     "ggk_work_shape_get": (_i, [_i, _i, _P(GGKWorkShape)]),
     "ggk_needs_addr64": (_i, [_i, _i, _P(GGDeviceProblemDesc)]),

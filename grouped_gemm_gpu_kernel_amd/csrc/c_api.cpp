@@ -167,19 +167,24 @@ int gg_executor_build(gg_executor* executor, const gg_problem_desc* sorted_probl
                       const int* tile_offsets, int offsets_len, int total_tiles,
                       const gg_kernel_config* config) {
   if (executor == nullptr) return hipErrorInvalidDevicePointer;
-  if (config == nullptr || bad_list(sorted_problems, count) || offsets_len < 0 ||
-      (offsets_len > 0 && tile_offsets == nullptr)) {
-    return hipErrorInvalidValue;
-  }
   try {
+    // Unusable arguments reach build() as an empty set or a rejected
+    // configuration, so that the executor records the failure (run() then
+    // refuses to launch) exactly as for any other rejected build.
+    gg::KernelConfig cpp_config;
+    cpp_config.threads = 0;
+    if (config != nullptr) cpp_config = to_cpp(*config);
     gg::PreparedProblemSet prepared;
-    prepared.sorted_problems = to_cpp(sorted_problems, count);
-    prepared.sorted_to_original.resize(count);
-    for (int i = 0; i < count; ++i) prepared.sorted_to_original[i] = i;
-    prepared.tile_offsets.assign(tile_offsets, tile_offsets + offsets_len);
-    prepared.total_tiles = total_tiles;
-    if (prepared.tile_offsets.empty()) return hipErrorInvalidValue;
-    return executor->executor.build(prepared, to_cpp(*config));
+    if (!bad_list(sorted_problems, count) && offsets_len > 0 && tile_offsets != nullptr) {
+      prepared.sorted_problems = to_cpp(sorted_problems, count);
+      prepared.sorted_to_original.resize(count);
+      for (int i = 0; i < count; ++i) prepared.sorted_to_original[i] = i;
+      prepared.tile_offsets.assign(tile_offsets, tile_offsets + offsets_len);
+      prepared.total_tiles = total_tiles;
+    }
+    const hipError_t status = executor->executor.build(prepared, cpp_config);
+    if (status == hipSuccess && config == nullptr) return hipErrorInvalidValue;
+    return status;
   } catch (...) {
     return hipErrorOutOfMemory;
   }

@@ -507,7 +507,16 @@ struct StageLoader<G, true> {
 // otherwise put a wait for every load in flight before each LDS read, which
 // serialises the stage pipeline.  Callers wait for these loads themselves
 // (wait_vmcnt); the compiler's own waits stay correct because loads complete
-// in order.  M0 holds the LDS address; nothing else in these kernels uses M0.
+// in order.  The LDS address is an operand bound to M0 ("{m0}"): the compiler
+// itself writes M0 before the statement and knows that it is read there, and
+// the statement changes no register.
+//
+// The compiler's hazard pass does not know that the statement is a
+// vector-memory instruction, so the statement provides the wait states the
+// hardware needs itself: a VALU write of an SGPR (v_readfirstlane of the
+// offset or of a resource word, which the compiler may place right before the
+// statement) needs 5 before a vector-memory instruction reads that SGPR, and
+// a SALU write of M0 needs 1 before an LDS load reads it.  s_nop 4 gives 5.
 __device__ __forceinline__ void load_to_lds16(const void* base, uint32_t num_records, uint32_t lds, uint32_t voff,
                                               uint32_t soff) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
@@ -516,9 +525,9 @@ __device__ __forceinline__ void load_to_lds16(const void* base, uint32_t num_rec
                         static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(num_records)), 0x00020000u};
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "{m0}"(m0), "v"(voff), "s"(rsrc), "s"(so)
                : "memory");
 }
 

@@ -483,6 +483,32 @@ hipError_t ggk_stream_synchronize(hipStream_t stream) { return hipStreamSynchron
 
 hipError_t ggk_device_synchronize(void) { return hipDeviceSynchronize(); }
 
+hipError_t ggk_event_create(hipEvent_t* event) {
+  if (event == nullptr) return hipErrorInvalidValue;
+  return hipEventCreateWithFlags(event, hipEventDisableTiming);
+}
+
+hipError_t ggk_event_destroy(hipEvent_t event) { return event == nullptr ? hipSuccess : hipEventDestroy(event); }
+
+hipError_t ggk_event_record_launch(hipEvent_t event, hipStream_t stream, int* recorded) {
+  if (recorded != nullptr) *recorded = 0;
+  if (event == nullptr) return hipErrorInvalidValue;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t st = hipStreamIsCapturing(stream, &capture);
+  if (st != hipSuccess) return st;
+  if (capture != hipStreamCaptureStatusNone) return hipSuccess;
+  st = hipEventRecord(event, stream);
+  if (st == hipSuccess && recorded != nullptr) *recorded = 1;
+  return st;
+}
+
+hipError_t ggk_event_synchronize(hipEvent_t event) { return event == nullptr ? hipSuccess : hipEventSynchronize(event); }
+
+hipError_t ggk_current_device(int* device) {
+  if (device == nullptr) return hipErrorInvalidValue;
+  return hipGetDevice(device);
+}
+
 hipError_t ggk_device_info_get(ggk_device_info* out) {
   if (out == nullptr) return hipErrorInvalidValue;
   int device = 0;

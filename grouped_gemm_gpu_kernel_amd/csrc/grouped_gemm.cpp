@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 #include <tuple>
 #include <utility>
@@ -45,13 +46,52 @@ struct RuntimeMode {
   ggk_work_shape work{};
 };
 
+// Per-process cache of what does not change while a process runs: each
+// device's properties and, per (device, variant, path), the kernel's
+// occupancy report.  The reference queries the device properties on every
+// build and occupancy query (src/grouped_gemm.cu:1141, 1222, 1032); here the
+// first call on a device pays for them.
+constexpr int kCachedDevices = 64;
+struct DeviceCache {
+  bool ready = false;
+  ggk_device_info info{};
+  bool occupancy_ready[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {};
+  OccupancyInfo occupancy[GGK_VARIANT_COUNT][GGK_PATH_COUNT];
+};
+std::mutex g_cache_mutex;
+DeviceCache g_device_cache[kCachedDevices];
+
+// The current device's cache entry (nullptr past kCachedDevices devices),
+// with its properties filled in.  Call with g_cache_mutex held.
+hipError_t device_cache(DeviceCache** out, ggk_device_info* info) {
+  *out = nullptr;
+  int device = 0;
+  hipError_t status = ggk_current_device(&device);
+  if (status != hipSuccess) return status;
+  if (device < 0 || device >= kCachedDevices) return ggk_device_info_get(info);
+  DeviceCache& c = g_device_cache[device];
+  if (!c.ready) {
+    status = ggk_device_info_get(&c.info);
+    if (status != hipSuccess) return status;
+    c.ready = true;
+  }
+  *info = c.info;
+  *out = &c;
+  return hipSuccess;
+}
+
 // resolve_runtime_mode (src/grouped_gemm.cu:111-143): unsupported shapes are
 // InvalidValue; the MFMA path is used when requested.  The library is built
 // for gfx950 only, where every accepted shape has an MFMA kernel.
 hipError_t resolve_runtime_mode(const KernelConfig& config, RuntimeMode* mode) {
   const int variant = resolve_variant(config);
   if (variant < 0) return hipErrorInvalidValue;
-  hipError_t status = ggk_device_info_get(&mode->device);
+  DeviceCache* cache = nullptr;
+  hipError_t status;
+  {
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    status = device_cache(&cache, &mode->device);
+  }
   if (status != hipSuccess) return status;
   mode->variant = variant;
   mode->path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;
@@ -138,6 +178,24 @@ hipError_t fill_occupancy(const KernelConfig& config, const RuntimeMode& mode, O
     info->theoretical_occupancy =
         static_cast<float>(info->active_warps_per_sm) / static_cast<float>(info->max_warps_per_sm);
   }
+  return hipSuccess;
+}
+
+// fill_occupancy through the per-process cache: the report depends only on
+// the device and the kernel (the variant fixes the macro-tile).
+hipError_t cached_occupancy(const KernelConfig& config, const RuntimeMode& mode, OccupancyInfo* info) {
+  std::lock_guard<std::mutex> lock(g_cache_mutex);
+  DeviceCache* cache = nullptr;
+  ggk_device_info dev{};
+  hipError_t status = device_cache(&cache, &dev);
+  if (status != hipSuccess) return status;
+  if (cache == nullptr) return fill_occupancy(config, mode, info);
+  if (!cache->occupancy_ready[mode.variant][mode.path]) {
+    status = fill_occupancy(config, mode, &cache->occupancy[mode.variant][mode.path]);
+    if (status != hipSuccess) return status;
+    cache->occupancy_ready[mode.variant][mode.path] = true;
+  }
+  *info = cache->occupancy[mode.variant][mode.path];
   return hipSuccess;
 }
 
@@ -231,17 +289,74 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
   return s;
 }
 
-void release(DeviceProblemDesc*& problems, int*& offsets, int*& state) {
-  if (problems == nullptr && offsets == nullptr && state == nullptr) return;
-  // Launches on any stream may still read these buffers: finish them first.
-  ggk_device_synchronize();
-  ggk_free(problems);
-  ggk_free(offsets);
-  ggk_free(state);
-  problems = nullptr;
-  offsets = nullptr;
-  state = nullptr;
-}
+// One device allocation per executor: descriptors, then ints, then the
+// scheduler state, each part starting on a 256-byte boundary (the state's
+// counters then sit on 128-byte lines of their own).  Launches read it until
+// they end, so it is rewritten or freed only after the last launch's event
+// (recorded on that launch's stream) has completed.
+struct DeviceBuffer {
+  void* base = nullptr;
+  size_t capacity = 0;  // bytes
+  int device = -1;
+  hipEvent_t last_launch = nullptr;
+  bool launched = false;  // an event was recorded since the last wait
+
+  static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+  hipError_t wait_launches() {
+    if (!launched) return hipSuccess;
+    launched = false;
+    return ggk_event_synchronize(last_launch);
+  }
+
+  // Records the event after a launch on `stream` (not while it is captured).
+  hipError_t note_launch(hipStream_t stream) {
+    if (last_launch == nullptr) return hipSuccess;
+    int recorded = 0;
+    const hipError_t status = ggk_event_record_launch(last_launch, stream, &recorded);
+    if (recorded) launched = true;
+    return status;
+  }
+
+  // At least `bytes` on the current device, reusing the allocation when it is
+  // large enough; waits for earlier launches either way.
+  hipError_t reserve(size_t bytes) {
+    hipError_t status = wait_launches();
+    if (status != hipSuccess) return status;
+    int current = 0;
+    status = ggk_current_device(&current);
+    if (status != hipSuccess) return status;
+    if (last_launch == nullptr || current != device) {
+      release();
+      status = ggk_event_create(&last_launch);
+      if (status != hipSuccess) return status;
+      device = current;
+    }
+    if (base != nullptr && capacity >= bytes) return hipSuccess;
+    (void)ggk_free(base);
+    base = nullptr;
+    capacity = 0;
+    status = ggk_alloc(&base, bytes);
+    if (status != hipSuccess) {
+      base = nullptr;
+      return status;
+    }
+    capacity = bytes;
+    return hipSuccess;
+  }
+
+  // Teardown: a failure here has nobody to report to.
+  void release() {
+    (void)wait_launches();
+    (void)ggk_free(base);
+    (void)ggk_event_destroy(last_launch);
+    base = nullptr;
+    capacity = 0;
+    device = -1;
+    last_launch = nullptr;
+    launched = false;
+  }
+};
 
 }  // namespace
 
@@ -349,21 +464,23 @@ hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info) {
   RuntimeMode mode;
   const hipError_t status = resolve_runtime_mode(config, &mode);
   if (status != hipSuccess) return status;
-  return fill_occupancy(config, mode, info);
+  return cached_occupancy(config, mode, info);
 }
 
 struct GroupedGemmExecutor::Impl {
+  DeviceBuffer buffer;
   DeviceProblemDesc* d_problems = nullptr;
-  int* d_tile_offsets = nullptr;  // [problem_count + 1] reference tile offsets, then
-                                  // [problem_count + 1] work-tile offsets in scheduling
-                                  // order, then [problem_count] the scheduling order,
-                                  // then (if work_table) [2 * total_work] the work table
+  // [problem_count + 1] reference tile offsets, then [problem_count + 1]
+  // work-tile offsets in scheduling order, then [problem_count] the
+  // scheduling order, then (if work_table) [2 * total_work] the work table.
+  int* d_ints = nullptr;
   int* d_state = nullptr;
 
   int problem_count = 0;
   int total_tiles = 0;
   int total_work = 0;
   int grid_ctas = 0;
+  bool failed = false;  // the last build() returned an error
 
   KernelConfig config{};
   int variant = -1;
@@ -373,20 +490,28 @@ struct GroupedGemmExecutor::Impl {
   bool work_table = false;
 
   const int* d_work_table() const {
-    return work_table ? d_tile_offsets + 3 * static_cast<size_t>(problem_count) + 2 : nullptr;
+    return work_table ? d_ints + 3 * static_cast<size_t>(problem_count) + 2 : nullptr;
+  }
+
+  // Forgets the last build (the buffer is kept for the next one).
+  void reset() {
+    d_problems = nullptr;
+    d_ints = nullptr;
+    d_state = nullptr;
+    problem_count = total_tiles = total_work = grid_ctas = 0;
+    variant = -1;
+    path = GGK_PATH_FMA;
+    addressing = GGK_ADDR_32;
+    chunk_bounds = {};
+    work_table = false;
   }
 };
 
 namespace {
 
 // Work tables up to this many work tiles (8 bytes each) are uploaded; larger
-// sets, and every set when the environment sets GG_WORK_TABLE=0, are searched.
+// sets are searched.
 constexpr int kWorkTableMax = 1 << 22;
-
-bool work_table_enabled() {
-  const char* v = std::getenv("GG_WORK_TABLE");
-  return v == nullptr || std::strcmp(v, "0") != 0;
-}
 
 }  // namespace
 
@@ -394,7 +519,7 @@ GroupedGemmExecutor::GroupedGemmExecutor() : impl_(new Impl()) {}
 
 GroupedGemmExecutor::~GroupedGemmExecutor() {
   if (impl_ != nullptr) {
-    release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
+    impl_->buffer.release();
     delete impl_;
     impl_ = nullptr;
   }
@@ -407,7 +532,7 @@ GroupedGemmExecutor::GroupedGemmExecutor(GroupedGemmExecutor&& other) noexcept :
 GroupedGemmExecutor& GroupedGemmExecutor::operator=(GroupedGemmExecutor&& other) noexcept {
   if (this != &other) {
     if (impl_ != nullptr) {
-      release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
+      impl_->buffer.release();
       delete impl_;
     }
     impl_ = other.impl_;
@@ -418,9 +543,15 @@ GroupedGemmExecutor& GroupedGemmExecutor::operator=(GroupedGemmExecutor&& other)
 
 // build (src/grouped_gemm.cu:1132-1239).  Beyond the reference's checks it
 // verifies that tile_offsets is the prefix sum of the sorted problems' tile
-// counts, so that a launch can never address a tile outside its problem.
+// counts, so that a launch can never address a tile outside its problem.  The
+// descriptors, offsets, schedule and zeroed scheduler state go to the device
+// in one copy, into the executor's allocation when it is large enough (after
+// the last run's launch has ended).  After a failed build, run() returns
+// hipErrorInvalidValue until a build succeeds.
 hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const KernelConfig& config) {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  impl_->reset();
+  impl_->failed = true;
 
   RuntimeMode mode;
   hipError_t status = resolve_runtime_mode(config, &mode);
@@ -429,9 +560,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   const int problem_count = static_cast<int>(prepared.sorted_problems.size());
   if (static_cast<int>(prepared.tile_offsets.size()) != problem_count + 1) return hipErrorInvalidValue;
   if (prepared.tile_offsets.back() != prepared.total_tiles) return hipErrorInvalidValue;
+  if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
 
-  release(impl_->d_problems, impl_->d_tile_offsets, impl_->d_state);
-  impl_->problem_count = problem_count;
   // A launch with few work tiles is bound by the latency of each tile's
   // stages rather than by bandwidth: when the 128 x 128 work tiles of the
   // small-set variants number at most two per workgroup slot (two
@@ -457,18 +587,9 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     }
   }
 
-  impl_->total_tiles = prepared.total_tiles;
-  impl_->total_work = 0;
-  impl_->grid_ctas = 0;
-  impl_->addressing = GGK_ADDR_32;
-  impl_->config = config;
-  impl_->variant = mode.variant;
-  impl_->path = mode.path;
-
+  int addressing = GGK_ADDR_32;
   std::vector<DeviceProblemDesc> device_problems;
   device_problems.reserve(problem_count);
-  std::vector<int> work(problem_count);
-  if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
   for (int i = 0; i < problem_count; ++i) {
     const ProblemDesc& p = prepared.sorted_problems[i];
     if (p.m < 0 || p.n < 0 || p.k < 0) return hipErrorInvalidValue;
@@ -478,21 +599,21 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
       return hipErrorInvalidValue;
     }
-    if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
+    if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) addressing = GGK_ADDR_64;
     device_problems.push_back(dp);
   }
   // The 64-bit form of the 256 x 256 work tile spills registers: a set that
   // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (impl_->addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
+  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
     mode.variant = GGK_VARIANT_128x64x32_SMALL;
     status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
     if (status != hipSuccess) return status;
-    impl_->variant = mode.variant;
-    impl_->addressing = GGK_ADDR_32;
+    addressing = GGK_ADDR_32;
     for (const DeviceProblemDesc& dp : device_problems) {
-      if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) impl_->addressing = GGK_ADDR_64;
+      if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) addressing = GGK_ADDR_64;
     }
   }
+  std::vector<int> work(problem_count);
   for (int i = 0; i < problem_count; ++i) {
     // Never above the problem's tile count, so the sums fit an int.
     const DeviceProblemDesc& dp = device_problems[i];
@@ -500,51 +621,59 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   }
   const Schedule schedule = plan_schedule(device_problems, work, config.cta_m * mode.work.tiles_m,
                                           config.cta_n * mode.work.tiles_n, mode.work.stage_k);
-  impl_->total_work = schedule.work_offsets.back();
-  impl_->chunk_bounds = schedule.bounds;
+  const int total_work = schedule.work_offsets.back();
+  const bool work_table = total_work > 0 && total_work <= kWorkTableMax;
+
+  OccupancyInfo occupancy{};
+  status = cached_occupancy(config, mode, &occupancy);
+  if (status != hipSuccess) return status;
+
   // Device ints: the reference tile offsets (sorted order), the work-tile
-  // offsets (scheduling order), the scheduling order.
-  std::vector<int> offsets(prepared.tile_offsets);
-  offsets.insert(offsets.end(), schedule.work_offsets.begin(), schedule.work_offsets.end());
-  offsets.insert(offsets.end(), schedule.order.begin(), schedule.order.end());
-  // The work table: (problem, work tile within it) of every work-tile index,
-  // so that the kernel reads it with one load instead of searching.
-  impl_->work_table = impl_->total_work > 0 && impl_->total_work <= kWorkTableMax && work_table_enabled();
-  if (impl_->work_table) {
-    offsets.reserve(offsets.size() + 2 * static_cast<size_t>(impl_->total_work));
+  // offsets (scheduling order), the scheduling order, then the work table --
+  // (problem, work tile within it) of every work-tile index, so that the
+  // kernel reads it with one load instead of searching.
+  const size_t int_count = 3 * static_cast<size_t>(problem_count) + 2 +
+                           (work_table ? 2 * static_cast<size_t>(total_work) : 0);
+  const size_t desc_bytes = DeviceBuffer::round256(problem_count * sizeof(DeviceProblemDesc));
+  const size_t int_bytes = DeviceBuffer::round256(int_count * sizeof(int));
+  const size_t state_bytes = DeviceBuffer::round256(GGK_SCHEDULER_STATE_INTS * sizeof(int));
+  const size_t total_bytes = desc_bytes + int_bytes + state_bytes;
+  std::vector<unsigned char> host(total_bytes, 0);
+  if (problem_count > 0) std::memcpy(host.data(), device_problems.data(), problem_count * sizeof(DeviceProblemDesc));
+  int* ints = reinterpret_cast<int*>(host.data() + desc_bytes);
+  ints = std::copy(prepared.tile_offsets.begin(), prepared.tile_offsets.end(), ints);
+  ints = std::copy(schedule.work_offsets.begin(), schedule.work_offsets.end(), ints);
+  ints = std::copy(schedule.order.begin(), schedule.order.end(), ints);
+  if (work_table) {
     for (const int prob : schedule.order) {
       for (int w = 0; w < work[prob]; ++w) {
-        offsets.push_back(prob);
-        offsets.push_back(w);
+        *ints++ = prob;
+        *ints++ = w;
       }
     }
   }
 
-  if (problem_count > 0) {
-    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems),
-                       problem_count * sizeof(DeviceProblemDesc));
-    if (status != hipSuccess) return status;
-    status = ggk_copy_to_device(impl_->d_problems, device_problems.data(),
-                                problem_count * sizeof(DeviceProblemDesc));
-    if (status != hipSuccess) return status;
-    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_tile_offsets), offsets.size() * sizeof(int));
-    if (status != hipSuccess) return status;
-    status = ggk_copy_to_device(impl_->d_tile_offsets, offsets.data(), offsets.size() * sizeof(int));
-    if (status != hipSuccess) return status;
-  }
-  if (impl_->total_tiles > 0) {
-    status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_state), GGK_SCHEDULER_STATE_INTS * sizeof(int));
-    if (status != hipSuccess) return status;
-    status = ggk_zero(impl_->d_state, GGK_SCHEDULER_STATE_INTS * sizeof(int));
-    if (status != hipSuccess) return status;
-  }
-
-
-  OccupancyInfo occupancy{};
-  status = fill_occupancy(config, mode, &occupancy);
+  status = impl_->buffer.reserve(total_bytes);
   if (status != hipSuccess) return status;
+  status = ggk_copy_to_device(impl_->buffer.base, host.data(), total_bytes);
+  if (status != hipSuccess) return status;
+
+  unsigned char* base = static_cast<unsigned char*>(impl_->buffer.base);
+  impl_->d_problems = reinterpret_cast<DeviceProblemDesc*>(base);
+  impl_->d_ints = reinterpret_cast<int*>(base + desc_bytes);
+  impl_->d_state = reinterpret_cast<int*>(base + desc_bytes + int_bytes);
+  impl_->problem_count = problem_count;
+  impl_->total_tiles = prepared.total_tiles;
+  impl_->total_work = total_work;
+  impl_->config = config;
+  impl_->variant = mode.variant;
+  impl_->path = mode.path;
+  impl_->addressing = addressing;
+  impl_->chunk_bounds = schedule.bounds;
+  impl_->work_table = work_table;
   // The persistent grid is sized by the units it claims: work tiles.
-  impl_->grid_ctas = grid_ctas_for(impl_->total_work, config, occupancy);
+  impl_->grid_ctas = grid_ctas_for(total_work, config, occupancy);
+  impl_->failed = false;
   return hipSuccess;
 }
 
@@ -553,22 +682,28 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
 // retires, so consecutive runs in stream order start from zero.
 hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  if (impl_->failed) return hipErrorInvalidValue;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
-  return ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                            impl_->d_tile_offsets + impl_->problem_count + 1,
-                            impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
-                            impl_->problem_count, impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(),
-                            impl_->grid_ctas, stream);
+  const hipError_t status =
+      ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
+                         impl_->d_ints + impl_->problem_count + 1, impl_->d_ints + 2 * (impl_->problem_count + 1),
+                         impl_->d_work_table(), impl_->problem_count, impl_->total_work, impl_->d_state,
+                         impl_->chunk_bounds.data(), impl_->grid_ctas, stream);
+  if (status != hipSuccess) return status;
+  return impl_->buffer.note_launch(stream);
 }
 
 hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  if (impl_->failed) return hipErrorInvalidValue;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
-  return ggk_launch_grouped_traced(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                                   impl_->d_tile_offsets, impl_->d_tile_offsets + impl_->problem_count + 1,
-                                   impl_->d_tile_offsets + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
-                                   impl_->problem_count, impl_->total_work, impl_->d_state,
-                                   impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map, d_wg_clock, stream);
+  const hipError_t status = ggk_launch_grouped_traced(
+      impl_->variant, impl_->path, impl_->addressing, impl_->d_problems, impl_->d_ints,
+      impl_->d_ints + impl_->problem_count + 1, impl_->d_ints + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
+      impl_->problem_count, impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map,
+      d_wg_clock, stream);
+  if (status != hipSuccess) return status;
+  return impl_->buffer.note_launch(stream);
 }
 
 int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }
@@ -593,7 +728,7 @@ hipError_t GroupedGemmExecutor::schedule(ggk_work_shape* shape, std::vector<int>
   // offsets, [count] scheduling order.
   std::vector<int> ints(count > 0 ? 3 * static_cast<size_t>(count) + 2 : 0);
   if (count > 0) {
-    const hipError_t status = ggk_copy_to_host(ints.data(), impl_->d_tile_offsets, ints.size() * sizeof(int));
+    const hipError_t status = ggk_copy_to_host(ints.data(), impl_->d_ints, ints.size() * sizeof(int));
     if (status != hipSuccess) return status;
   }
   if (work_offsets != nullptr) {
@@ -655,6 +790,7 @@ struct MoeGroupedGemm::Impl {
   int addressing = GGK_ADDR_32;
   int sort_mode = 0;
   int grid_ctas = 0;
+  DeviceBuffer buffer;
   DeviceProblemDesc* d_problems = nullptr;
   int* d_ints = nullptr;  // offsets [2 * (E + 1)] | permutation [E] | order [E] | header
   int* d_state = nullptr;
@@ -663,13 +799,23 @@ struct MoeGroupedGemm::Impl {
   int* perm() const { return d_ints + 2 * (layout.experts + 1); }
   int* order() const { return perm() + layout.experts; }
   int* header() const { return order() + layout.experts; }
+
+  // Forgets the last build: run() refuses to launch until a build succeeds.
+  void reset() {
+    layout = ggk_moe_layout{};
+    variant = -1;
+    grid_ctas = 0;
+    d_problems = nullptr;
+    d_ints = nullptr;
+    d_state = nullptr;
+  }
 };
 
 MoeGroupedGemm::MoeGroupedGemm() : impl_(new Impl()) {}
 
 MoeGroupedGemm::~MoeGroupedGemm() {
   if (impl_ != nullptr) {
-    release(impl_->d_problems, impl_->d_ints, impl_->d_state);
+    impl_->buffer.release();
     delete impl_;
     impl_ = nullptr;
   }
@@ -680,7 +826,7 @@ MoeGroupedGemm::MoeGroupedGemm(MoeGroupedGemm&& other) noexcept : impl_(other.im
 MoeGroupedGemm& MoeGroupedGemm::operator=(MoeGroupedGemm&& other) noexcept {
   if (this != &other) {
     if (impl_ != nullptr) {
-      release(impl_->d_problems, impl_->d_ints, impl_->d_state);
+      impl_->buffer.release();
       delete impl_;
     }
     impl_ = other.impl_;
@@ -689,8 +835,13 @@ MoeGroupedGemm& MoeGroupedGemm::operator=(MoeGroupedGemm&& other) noexcept {
   return *this;
 }
 
+// Checks the layout and sizes the device-side set: E descriptors, 2 (E + 1) +
+// 2 E + GGK_MOE_HEADER_INTS ints and the scheduler state, in one allocation
+// (kept from the previous build when large enough).  On any failure the
+// object is reset and run() returns hipErrorInvalidDevicePointer.
 hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode) {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  impl_->reset();
   RuntimeMode mode;
   hipError_t status = resolve_runtime_mode(config, &mode);
   if (status != hipSuccess) return status;
@@ -744,22 +895,23 @@ hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& co
     wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   }
 
-  release(impl_->d_problems, impl_->d_ints, impl_->d_state);
-  const size_t ints = 2 * static_cast<size_t>(e + 1) + 2 * static_cast<size_t>(e) + GGK_MOE_HEADER_INTS;
-  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_problems), e * sizeof(DeviceProblemDesc));
-  if (status != hipSuccess) return status;
-  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_ints), ints * sizeof(int));
-  if (status != hipSuccess) return status;
-  status = ggk_zero(impl_->d_ints, ints * sizeof(int));
-  if (status != hipSuccess) return status;
-  status = ggk_alloc(reinterpret_cast<void**>(&impl_->d_state), GGK_SCHEDULER_STATE_INTS * sizeof(int));
-  if (status != hipSuccess) return status;
-  status = ggk_zero(impl_->d_state, GGK_SCHEDULER_STATE_INTS * sizeof(int));
+  OccupancyInfo occupancy{};
+  status = cached_occupancy(config, mode, &occupancy);
   if (status != hipSuccess) return status;
 
-  OccupancyInfo occupancy{};
-  status = fill_occupancy(config, mode, &occupancy);
+  const size_t ints = 2 * static_cast<size_t>(e + 1) + 2 * static_cast<size_t>(e) + GGK_MOE_HEADER_INTS;
+  const size_t desc_bytes = DeviceBuffer::round256(e * sizeof(DeviceProblemDesc));
+  const size_t int_bytes = DeviceBuffer::round256(ints * sizeof(int));
+  const size_t state_bytes = DeviceBuffer::round256(GGK_SCHEDULER_STATE_INTS * sizeof(int));
+  status = impl_->buffer.reserve(desc_bytes + int_bytes + state_bytes);
   if (status != hipSuccess) return status;
+  status = ggk_zero(impl_->buffer.base, desc_bytes + int_bytes + state_bytes);
+  if (status != hipSuccess) return status;
+
+  unsigned char* base = static_cast<unsigned char*>(impl_->buffer.base);
+  impl_->d_problems = reinterpret_cast<DeviceProblemDesc*>(base);
+  impl_->d_ints = reinterpret_cast<int*>(base + desc_bytes);
+  impl_->d_state = reinterpret_cast<int*>(base + desc_bytes + int_bytes);
   impl_->layout = L;
   impl_->variant = mode.variant;
   impl_->path = mode.path;
@@ -774,23 +926,27 @@ hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& co
 }
 
 hipError_t MoeGroupedGemm::run(const int* d_counts, hipStream_t stream) const {
-  if (impl_ == nullptr || impl_->d_problems == nullptr) return hipErrorInvalidDevicePointer;
+  if (impl_ == nullptr || impl_->d_problems == nullptr || impl_->variant < 0) return hipErrorInvalidDevicePointer;
   if (d_counts == nullptr) return hipErrorInvalidDevicePointer;
   hipError_t status = ggk_moe_prepare(impl_->variant, impl_->path, &impl_->layout, d_counts, impl_->sort_mode,
                                       impl_->d_problems, impl_->offsets(), impl_->perm(), impl_->order(),
                                       impl_->header(), stream);
   if (status != hipSuccess) return status;
-  return ggk_launch_grouped_device(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
-                                   impl_->offsets() + impl_->layout.experts + 1, impl_->order(),
-                                   impl_->layout.experts, impl_->header(), impl_->d_state, impl_->grid_ctas,
-                                   stream);
+  status = ggk_launch_grouped_device(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
+                                     impl_->offsets() + impl_->layout.experts + 1, impl_->order(),
+                                     impl_->layout.experts, impl_->header(), impl_->d_state, impl_->grid_ctas,
+                                     stream);
+  if (status != hipSuccess) return status;
+  return impl_->buffer.note_launch(stream);
 }
 
 int MoeGroupedGemm::grid_ctas() const { return impl_ != nullptr ? impl_->grid_ctas : 0; }
 const DeviceProblemDesc* MoeGroupedGemm::device_problems() const {
   return impl_ != nullptr ? impl_->d_problems : nullptr;
 }
-const int* MoeGroupedGemm::device_offsets() const { return impl_ != nullptr && impl_->d_ints ? impl_->offsets() : nullptr; }
+const int* MoeGroupedGemm::device_offsets() const {
+  return impl_ != nullptr && impl_->d_ints ? impl_->offsets() : nullptr;
+}
 const int* MoeGroupedGemm::device_sorted_to_original() const {
   return impl_ != nullptr && impl_->d_ints ? impl_->perm() : nullptr;
 }

@@ -128,6 +128,22 @@ hipError_t ggk_zero(void* ptr, size_t bytes);
 hipError_t ggk_stream_synchronize(hipStream_t stream);
 hipError_t ggk_device_synchronize(void);
 
+/* Completion tracking of an executor's launches (no reference counterpart: the
+ * reference frees its buffers with cudaFree, which waits for the whole device).
+ * An executor records its event after each launch on the launch's stream --
+ * not while that stream is being captured into a graph -- and waits for it
+ * before it rewrites or frees the buffers those launches read.  Events are
+ * created with timing disabled. */
+hipError_t ggk_event_create(hipEvent_t* event);
+hipError_t ggk_event_destroy(hipEvent_t event);
+/* Records `event` on `stream` unless the stream is capturing; *recorded (may
+ * be NULL) tells which. */
+hipError_t ggk_event_record_launch(hipEvent_t event, hipStream_t stream, int* recorded);
+hipError_t ggk_event_synchronize(hipEvent_t event);
+
+/* Index of the current device (hipGetDevice). */
+hipError_t ggk_current_device(int* device);
+
 /* Device properties of the current device (cudaGetDeviceProperties in
  * resolve_runtime_mode and query_occupancy, src/grouped_gemm.cu:111-143,
  * 1024-1083). */

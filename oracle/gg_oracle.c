@@ -376,6 +376,14 @@ float go_gemm_element(int i, int j, int k, const uint16_t* a, int lda, const uin
   return lhs + rhs;
 }
 
+void go_gemm_samples(int count, const int* k, const uint16_t* a, const int64_t* a_start, const uint16_t* b,
+                     const int64_t* b_start, const float* c, const float* alpha, const float* beta, float* out) {
+  for (int s = 0; s < count; ++s) {
+    out[s] = go_gemm_element(0, 0, k[s], a + a_start[s], 1, b + b_start[s], 1, c != NULL ? c + s : NULL, 1,
+                             alpha[s], beta[s]);
+  }
+}
+
 void go_gemm(int m, int n, int k, const uint16_t* a, int lda, const uint16_t* b, int ldb,
              const float* c, int ldc, float alpha, float beta, float* d, int ldd) {
   if (m <= 0 || n <= 0) return;

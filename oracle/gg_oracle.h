@@ -117,6 +117,13 @@ void go_gemm_omp(int m, int n, int k, const uint16_t* a, int lda, const uint16_t
 /* One element (i, j) of go_gemm. */
 float go_gemm_element(int i, int j, int k, const uint16_t* a, int lda, const uint16_t* b, int ldb,
                       const float* c, int ldc, float alpha, float beta);
+/* count independent elements of go_gemm, each given as its own row of A and
+ * column of B: element s takes k[s] values from a + a_start[s] and
+ * b + b_start[s] (both contiguous), c[s] (c may be NULL: 0), alpha[s] and
+ * beta[s], with go_gemm_element's arithmetic in the same order; results to
+ * out[s].  Pinned against go_gemm bit for bit (tests/test_oracle.py). */
+void go_gemm_samples(int count, const int* k, const uint16_t* a, const int64_t* a_start, const uint16_t* b,
+                     const int64_t* b_start, const float* c, const float* alpha, const float* beta, float* out);
 
 /* ---- Metric helpers (bench/benchmark_grouped_gemm.cu:570-607). ----------- */
 double go_total_flops(int count, const int* m, const int* n, const int* k);

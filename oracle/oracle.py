@@ -52,6 +52,7 @@ _SIGS = {
                            _i]),
     "go_gemm_element": (ctypes.c_float, [_i, _i, _i, _u16p, _i, _u16p, _i, _fp, _i, ctypes.c_float,
                                          ctypes.c_float]),
+    "go_gemm_samples": (None, [_i, _ip, _u16p, _i64p, _u16p, _i64p, _fp, _fp, _fp, _fp]),
     "go_total_flops": (ctypes.c_double, [_i, _ip, _ip, _ip]),
     "go_tail_work_share": (ctypes.c_double, [_i, _ip, _ip, _i]),
     "go_omp_max_threads": (_i, []),
@@ -221,6 +222,30 @@ def gemm_element(i: int, j: int, k: int, a: np.ndarray, lda: int, b: np.ndarray,
         c = np.ascontiguousarray(c, dtype=np.float32)
         cp = _p(c, _fp)
     return lib().go_gemm_element(i, j, k, _p(a, _u16p), lda, _p(b, _u16p), ldb, cp, ldc, alpha, beta)
+
+
+def gemm_samples(k, a: np.ndarray, a_start, b: np.ndarray, b_start, c, alpha, beta) -> np.ndarray:
+    """Elements of the reference host GEMM given as (row of A, column of B) pairs: sample s is
+    alpha[s] * sum_kk A[kk] B[kk] + beta[s] * c[s] over k[s] values at a[a_start[s]:] and
+    b[b_start[s]:] (go_gemm_samples)."""
+    k = _ints(k)
+    cnt = k.size
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    a_start = np.ascontiguousarray(a_start, dtype=np.int64)
+    b_start = np.ascontiguousarray(b_start, dtype=np.int64)
+    assert a_start.size == cnt and b_start.size == cnt
+    assert cnt == 0 or (int((a_start + k).max()) <= a.size and int((b_start + k).max()) <= b.size)
+    alpha = np.ascontiguousarray(alpha, dtype=np.float32)
+    beta = np.ascontiguousarray(beta, dtype=np.float32)
+    cp = None
+    if c is not None:
+        c = np.ascontiguousarray(c, dtype=np.float32)
+        cp = _p(c, _fp)
+    out = np.zeros(max(1, cnt), np.float32)
+    lib().go_gemm_samples(cnt, _p(k, _ip), _p(a, _u16p), _p(a_start, _i64p), _p(b, _u16p), _p(b_start, _i64p), cp,
+                          _p(alpha, _fp), _p(beta, _fp), _p(out, _fp))
+    return out[:cnt]
 
 
 def total_flops(m, n, k) -> float:

@@ -101,3 +101,65 @@ def test_addressing_form_classifier():
     assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (1, 2, 256, 128, 64)
     assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_64x128x32_SMALL, _lib.GGK_PATH_MFMA, shape) == 0
     assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 1, 256, 128, 64)
+
+
+def test_failed_build_blocks_run():
+    """After a rejected build the executor refuses to launch (hipErrorInvalidValue) instead of running
+    a half-configured set; a never-built executor runs nothing and succeeds, as in the reference.
+    Unsupported configurations and unusable argument lists are rejected before any device call, so
+    this runs without a GPU."""
+    import ctypes
+
+    lib = _lib.lib()
+    ex = lib.gg_executor_create()
+    try:
+        assert lib.gg_executor_run(ex, None) == _lib.HIP_SUCCESS
+        bad_cfg = _lib.GGKernelConfig(128, 64, 32, 128, 0, 1)  # threads must be 256
+        probs = (_lib.GGProblemDesc * 1)(_lib.GGProblemDesc(4, 4, 4, 0x1000, 0x2000, None, 0x3000, 4, 4, 4, 4,
+                                                            1.0, 0.0))
+        offs = (ctypes.c_int * 2)(0, 1)
+        assert lib.gg_executor_build(ex, probs, 1, offs, 2, 1, ctypes.byref(bad_cfg)) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_run(ex, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_run_traced(ex, None, None, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_total_tiles(ex) == 0 and lib.gg_executor_problem_count(ex) == 0
+        # a NULL problem list with a non-zero count and a NULL config are rejected the same way
+        assert lib.gg_executor_build(ex, None, 3, offs, 2, 1, ctypes.byref(bad_cfg)) != _lib.HIP_SUCCESS
+        assert lib.gg_executor_run(ex, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_build(ex, probs, 1, offs, 2, 1, None) != _lib.HIP_SUCCESS
+        assert lib.gg_executor_run(ex, None) == _lib.HIP_ERROR_INVALID_VALUE
+    finally:
+        lib.gg_executor_destroy(ex)
+
+
+def _gfx950_disassembly(tmp_path) -> str:
+    """AMD assembly of the library's first gfx950 code object (the GEMM kernels), from its
+    .hip_fatbin section."""
+    llvm = Path("/opt/rocm/llvm/bin")
+    fatbin = tmp_path / "fatbin.bin"
+    subprocess.run([str(llvm / "llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", str(_lib.LIB_PATH),
+                    str(tmp_path / "copy.so")], check=True, capture_output=True)
+    code = tmp_path / "gfx950.o"
+    subprocess.run([str(llvm / "clang-offload-bundler"), "--unbundle", "--type=o",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fatbin}", f"--output={code}"],
+                   check=True, capture_output=True)
+    return subprocess.run([str(llvm / "llvm-objdump"), "-d", "--mcpu=gfx950", str(code)], check=True,
+                          capture_output=True, text=True).stdout
+
+
+def test_lds_loads_carry_their_wait_states(tmp_path):
+    """The global -> LDS loads are inline assembly, which the compiler's hazard pass does not treat as
+    memory instructions, so each must bring its own wait states: a VALU write of an SGPR the load
+    reads (offset, resource words; v_readfirstlane right before the statement) needs 5, a SALU write
+    of M0 needs 1.  Every `buffer_load_dwordx4 ... lds` of the built code must directly follow
+    `s_nop N` with N >= 4 (N + 1 wait states)."""
+    dis = _gfx950_disassembly(tmp_path)
+    ins = [ln.split("//")[0].strip() for ln in dis.splitlines() if ln.startswith("\t")]
+    ins = [x for x in ins if x]
+    loads = [i for i, x in enumerate(ins) if x.startswith("buffer_load_dwordx4") and x.endswith(" lds")]
+    assert len(loads) > 100, "expected the LDS-DMA loads of the MFMA kernels"
+    bad = []
+    for i in loads:
+        prev = ins[i - 1].split()
+        if not (prev[0] == "s_nop" and int(prev[1], 0) >= 4):
+            bad.append(ins[i - 3:i + 1])
+    assert not bad, f"{len(bad)} LDS loads without wait states, e.g. {bad[0]}"

@@ -5,9 +5,9 @@ Bars:
   * D: max |D - D_oracle| <= 1e-3 * sqrt(K) * max|A| * max|B| * |alpha| + 1e-6 * (|beta| * max|C| + 1)
     per problem (the BASELINE bound with |alpha| included, plus a few float32 ulps of the beta*C term).
   * D is NaN-poisoned before every run, so a tile that is skipped cannot pass on stale output.
-  * Full-size sets: every sort mode and the per-problem baseline give bit-identical D (each tile's
-    arithmetic does not depend on which workgroup runs it), checked against the oracle on samples.
+  * Full-size sets of every benchmark workload: tests/test_full_size.py.
 """
+import ctypes
 import math
 import os
 import subprocess
@@ -167,20 +167,65 @@ def _mapping_sets():
     return sets
 
 
+def _variant_of(cfg, shape):
+    """The kernel variant build() chose: the configuration's own or its small-set form, told apart
+    by the work shape."""
+    base = {(64, 64): _lib.GGK_VARIANT_64x64x16, (128, 64): _lib.GGK_VARIANT_128x64x32,
+            (64, 128): _lib.GGK_VARIANT_64x128x32}[(cfg.cta_m, cfg.cta_n)]
+    small = {_lib.GGK_VARIANT_128x64x32: _lib.GGK_VARIANT_128x64x32_SMALL,
+             _lib.GGK_VARIANT_64x128x32: _lib.GGK_VARIANT_64x128x32_SMALL}.get(base)
+    for v in (base, small):
+        if v is None:
+            continue
+        ws = _lib.GGKWorkShape()
+        _lib.check(_lib.lib().ggk_work_shape_get(v, _lib.GGK_PATH_MFMA, ctypes.byref(ws)), "work shape")
+        if (ws.tiles_m, ws.tiles_n) == (shape.tiles_m, shape.tiles_n):
+            return v
+    raise AssertionError(f"no variant of {cfg} has work shape {shape.tiles_m}x{shape.tiles_n}")
+
+
+def _traced_map_by_search(torch, ex, prep, cfg):
+    """The traced tile map of the executor's schedule launched through the kernel C-ABI with no work
+    table, so that the kernel finds each claimed index's problem with its own search over the
+    work-tile offsets (the device-side prepare's form)."""
+    shape, order, offsets, bounds = ex.schedule()
+    count = len(prep.sorted_problems)
+    descs = (_lib.GGDeviceProblemDesc * max(1, count))()
+    for i, p in enumerate(prep.sorted_problems):
+        live = p.m > 0 and p.n > 0
+        descs[i] = _lib.GGDeviceProblemDesc(p.m, p.n, p.k, p.a or None, p.b or None, p.c or None, p.d or None,
+                                            p.lda, p.ldb, p.ldc, p.ldd, p.alpha, p.beta,
+                                            -(-p.m // cfg.cta_m) if live else 0, -(-p.n // cfg.cta_n) if live else 0)
+    d_desc = torch.empty(ctypes.sizeof(descs), dtype=torch.uint8, device="cuda")
+    _lib.check(_lib.lib().ggk_copy_to_device(d_desc.data_ptr(), ctypes.addressof(descs), ctypes.sizeof(descs)),
+               "descriptors")
+    d_tiles = torch.tensor(prep.tile_offsets, dtype=torch.int32, device="cuda")
+    d_work = torch.tensor(offsets, dtype=torch.int32, device="cuda")
+    d_order = torch.tensor(order if order else [0], dtype=torch.int32, device="cuda")
+    d_state = torch.zeros(_lib.GGK_SCHEDULER_STATE_INTS, dtype=torch.int32, device="cuda")
+    total = prep.total_tiles
+    tmap = torch.full((3 * max(1, total),), -1, dtype=torch.int32, device="cuda")
+    c_bounds = (ctypes.c_int * len(bounds))(*bounds)
+    st = _lib.lib().ggk_launch_grouped_traced(_variant_of(cfg, shape), _lib.GGK_PATH_MFMA, _lib.GGK_ADDR_32,
+                                              d_desc.data_ptr(), d_tiles.data_ptr(), d_work.data_ptr(),
+                                              d_order.data_ptr(), None, count, offsets[-1], d_state.data_ptr(),
+                                              c_bounds, ex.grid_ctas(), tmap.data_ptr(), None, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    return tmap.cpu().numpy()[:3 * total].reshape(total, 3)
+
+
 @pytest.mark.parametrize("config", CONFIGS)
-@pytest.mark.parametrize("work_table", [True, False])
-def test_tile_mapping_bit_exact(torch, config, work_table, monkeypatch):
+def test_tile_mapping_bit_exact(torch, config):
     """The scheduler's tile -> (problem, tile_m, tile_n) function equals find_problem_by_tile plus the
     row-major local tile (src/grouped_gemm.cu:219-234, 659-668), for every claimed index: read from
-    the executor's work table, and found by the kernel's own search (GG_WORK_TABLE=0 at build)."""
-    if not work_table:
-        monkeypatch.setenv("GG_WORK_TABLE", "0")
+    the executor's work table, and found by the kernel's own search when launched without one."""
     cfg = KernelConfig.named(config)
     for name, shapes in _mapping_sets().items():
         shapes = [(int(a), int(b), int(c)) for a, b, c in shapes]
         buf, probs = _dummy_problems(torch, shapes)
         for mode in (SortMode.kNone, SortMode.kByK, SortMode.kByTiles):
-            say(f"mapping {config} {name} mode={int(mode)} work_table={work_table}")
+            say(f"mapping {config} {name} mode={int(mode)}")
             prep = api.prepare_problem_set(probs, cfg, mode)
             ex = GroupedGemmExecutor()
             assert ex.build(prep, cfg) == 0
@@ -193,7 +238,9 @@ def test_tile_mapping_bit_exact(torch, config, work_table, monkeypatch):
             sn = np.array([p.n for p in prep.sorted_problems])
             tiles_n = np.where((sm > 0) & (sn > 0), (sn + cfg.cta_n - 1) // cfg.cta_n, 1)
             want = O.map_tiles(tiles_n, prep.tile_offsets)
-            assert np.array_equal(got, want), f"{config} {name} mode {mode}"
+            assert np.array_equal(got, want), f"{config} {name} mode {mode} (work table)"
+            assert np.array_equal(_traced_map_by_search(torch, ex, prep, cfg), want), \
+                f"{config} {name} mode {mode} (search)"
             ex.close()
         del buf
 
@@ -566,53 +613,6 @@ def test_wall_clock_trace(torch):
     c = clock.cpu().numpy().reshape(-1, 2)
     assert (c[:, 0] > 0).all() and (c[:, 1] >= c[:, 0]).all()
     assert c[:, 1].max() - c[:, 0].min() < 100_000_000  # under a second at 100 MHz
-
-
-@pytest.mark.parametrize("name", ["mixed512"])
-def test_full_size_modes_identical_and_sampled(torch, name):
-    """mixed-512 at full size: the 4 sort modes and the baseline give bit-identical D; sampled elements
-    and a few whole problems match the oracle."""
-    say(f"full size {name}")
-    spec = make_spec(name)
-    dw = DeviceWorkload(spec)
-    probs = dw.problems()
-    cfg = KernelConfig.named(spec.config)
-    ref = None
-    for mode in list(SortMode) + ["baseline"]:
-        dw.poison_d()
-        if mode == "baseline":
-            assert api.run_baseline_per_problem(probs, cfg) == 0
-        else:
-            prep = api.prepare_problem_set(probs, cfg, mode)
-            ex = GroupedGemmExecutor()
-            assert ex.build(prep, cfg) == 0
-            assert ex.run() == 0
-            torch.cuda.synchronize()
-            ex.close()
-        torch.cuda.synchronize()
-        d = dw.d.cpu().numpy()
-        if ref is None:
-            ref = d
-        else:
-            assert np.array_equal(d.view(np.uint32), ref.view(np.uint32)), f"mode {mode} differs"
-    rng = np.random.default_rng(21)
-    for i in rng.choice(spec.count, 48, replace=False):
-        p = probs[i]
-        rows = rng.integers(0, p.m, 6)
-        cols = rng.integers(0, p.n, 6)
-        ar = dw.host_a_rows(i, rows)
-        bc = dw.host_b_cols(i, cols)
-        c = dw.host_c(i)
-        d = dw.host_d(i)
-        for r_i, r in enumerate(rows):
-            for c_i, col in enumerate(cols):
-                want = O.gemm_element(0, 0, p.k, ar[r_i], p.k, np.ascontiguousarray(bc[:, c_i]), 1,
-                                      c[r * p.ldc + col:], 1, p.alpha, p.beta)
-                assert abs(d[r * p.ldd + col] - want) <= tolerance(p.k, 1.0, 1.0, 1.0, p.alpha, p.beta), (i, r, col)
-    for i in np.argsort(spec.m * spec.n)[:3]:
-        p = probs[i]
-        want = O.gemm(p.m, p.n, p.k, dw.host_a(i), p.lda, dw.host_b(i), p.ldb, dw.host_c(i), p.ldc, p.alpha, p.beta)
-        assert np.abs(dw.host_d(i)[:p.m * p.n] - want[:p.m * p.n]).max() <= tolerance(p.k, 1, 1, 1, p.alpha, p.beta)
 
 
 def test_cpp_dropin_driver(torch):

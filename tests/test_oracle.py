@@ -354,3 +354,44 @@ def test_total_flops_and_tail_share_closed_form():
     share = O.tail_work_share(k, offs, 32)
     assert share == pytest.approx((19 + 20) / sum(range(1, 21)))
     assert O.tail_work_share([], [0], 16) == 0.0
+
+
+def test_gemm_samples_equal_gemm():
+    """go_gemm_samples (each element from its own row of A and column of B, gathered out of the
+    matrices) gives go_gemm's element bit for bit, per-sample alpha/beta and C included; a sample with
+    k = 0 is beta * c.  A plausible slip -- a dropped last product, reversed k order, alpha and beta
+    swapped -- changes the bits of some of the 400 samples."""
+    rng = np.random.default_rng(8)
+    shapes = [(23, 17, 129), (5, 40, 1), (9, 9, 0), (31, 12, 1000)]
+    ks, a_parts, b_parts, a_start, b_start, cs, alphas, betas, want = [], [], [], [], [], [], [], [], []
+    a_len = b_len = 0
+    for (m, n, k) in shapes:
+        a = _rand_half(rng, max(1, m * k))
+        b = _rand_half(rng, max(1, k * n))
+        c = rng.uniform(-1, 1, m * n).astype(np.float32)
+        alpha, beta = float(rng.uniform(0.5, 2)), float(rng.uniform(0, 1))
+        d = O.gemm(m, n, k, a, max(1, k), b, n, c, n, alpha, beta)
+        for _ in range(100):
+            i, j = int(rng.integers(0, m)), int(rng.integers(0, n))
+            row = a[i * k:(i + 1) * k] if k > 0 else np.zeros(0, np.uint16)
+            col = b[j::n][:k] if k > 0 else np.zeros(0, np.uint16)
+            ks.append(k)
+            a_start.append(a_len)
+            b_start.append(b_len)
+            a_parts.append(row)
+            b_parts.append(col)
+            a_len += row.size
+            b_len += col.size
+            cs.append(c[i * n + j])
+            alphas.append(alpha)
+            betas.append(beta)
+            want.append(d[i * n + j])
+    got = O.gemm_samples(ks, np.concatenate(a_parts), a_start, np.concatenate(b_parts), b_start, np.array(cs),
+                         alphas, betas)
+    assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32))
+    # no C: the beta term reads as 0
+    got0 = O.gemm_samples(ks[:5], np.concatenate(a_parts), a_start[:5], np.concatenate(b_parts), b_start[:5], None,
+                          alphas[:5], betas[:5])
+    for s in range(5):
+        e = O.gemm_element(0, 0, ks[s], a_parts[s], 1, b_parts[s], 1, None, 1, alphas[s], betas[s])
+        assert np.float32(e).view(np.uint32) == got0[s].view(np.uint32)

@@ -38,6 +38,7 @@ GGK_MOE_HEADER_INTS = 16
 GGK_MOE_STATUS = 12
 GGK_MOE_NEGATIVE = 1
 GGK_MOE_CLAMPED = 2
+GG_MOE_NOALLOC_SCRATCH_BYTES = 99840
 
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_ll_p = ctypes.POINTER(ctypes.c_longlong)
@@ -143,6 +144,7 @@ SIGNATURES = {
     "gg_moe_grid_ctas": (_i, [_vp]),
     "gg_moe_device_buffers": (_i, [_vp, _P(_vp), _P(_vp), _P(_vp), _P(_vp), _P(_vp)]),
     "gg_moe_destroy": (None, [_vp]),
+    "gg_moe_run_noalloc": (_i, [_P(GGKMoeLayout), _P(GGKernelConfig), _i, _vp, _vp]),
     # grouped_gemm_amd_kernels.h
     "ggk_alloc": (_i, [_P(_vp), ctypes.c_size_t]),
     "ggk_free": (_i, [_vp]),

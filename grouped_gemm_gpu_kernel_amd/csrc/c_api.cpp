@@ -87,6 +87,26 @@ std::vector<gg::ProblemDesc> to_cpp(const gg_problem_desc* problems, int count) 
   return out;
 }
 
+gg::MoeLayout to_cpp(const ggk_moe_layout& layout) {
+  gg::MoeLayout L;
+  L.experts = layout.experts;
+  L.n = layout.n;
+  L.k = layout.k;
+  L.a = static_cast<const __half*>(layout.a);
+  L.lda = layout.lda;
+  L.b = static_cast<const __half*>(layout.b);
+  L.ldb = layout.ldb;
+  L.stride_b = layout.stride_b;
+  L.c = layout.c;
+  L.ldc = layout.ldc;
+  L.d = layout.d;
+  L.ldd = layout.ldd;
+  L.alpha = layout.alpha;
+  L.beta = layout.beta;
+  L.max_rows = layout.max_rows;
+  return L;
+}
+
 bool bad_list(const gg_problem_desc* problems, int count) {
   return count < 0 || (count > 0 && problems == nullptr);
 }
@@ -270,22 +290,7 @@ int gg_moe_create(const ggk_moe_layout* layout, const gg_kernel_config* config, 
   if (layout == nullptr || config == nullptr) return hipErrorInvalidValue;
   gg_moe* m = new (std::nothrow) gg_moe;
   if (m == nullptr) return hipErrorOutOfMemory;
-  gg::MoeLayout L;
-  L.experts = layout->experts;
-  L.n = layout->n;
-  L.k = layout->k;
-  L.a = static_cast<const __half*>(layout->a);
-  L.lda = layout->lda;
-  L.b = static_cast<const __half*>(layout->b);
-  L.ldb = layout->ldb;
-  L.stride_b = layout->stride_b;
-  L.c = layout->c;
-  L.ldc = layout->ldc;
-  L.d = layout->d;
-  L.ldd = layout->ldd;
-  L.alpha = layout->alpha;
-  L.beta = layout->beta;
-  L.max_rows = layout->max_rows;
+  const gg::MoeLayout L = to_cpp(*layout);
   const hipError_t status = m->moe.build(L, to_cpp(*config), static_cast<gg::SortMode>(sort_mode));
   if (status != hipSuccess) {
     delete m;
@@ -314,5 +319,12 @@ int gg_moe_device_buffers(const gg_moe* moe, const gg_device_problem_desc** prob
 }
 
 void gg_moe_destroy(gg_moe* moe) { delete moe; }
+
+int gg_moe_run_noalloc(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode,
+                       const int* d_counts, hipStream_t stream) {
+  if (layout == nullptr || config == nullptr) return hipErrorInvalidValue;
+  const gg::MoeLayout L = to_cpp(*layout);
+  return gg::run_moe_grouped_gemm_noalloc(L, to_cpp(*config), static_cast<gg::SortMode>(sort_mode), d_counts, stream);
+}
 
 }  // extern "C"

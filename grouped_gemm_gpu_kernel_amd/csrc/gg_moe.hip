@@ -12,6 +12,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
+#include "grouped_gemm_amd.h"
 #include "grouped_gemm_amd_kernels.h"
 
 namespace {
@@ -339,6 +342,53 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
 constexpr int kCta[GGK_VARIANT_COUNT][2] = {{64, 64}, {128, 64}, {64, 128}, {128, 64}, {64, 128}};
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free MoE entry point (gg_moe_run_noalloc): the
+// prepared set of up to GGK_MOE_MAX_EXPERTS experts -- descriptors, offsets,
+// permutation, scheduling order, header -- and the scheduler state, laid out
+// as gg_moe_scratch_layout describes.  Every GPU holds one copy for the life
+// of the process, shared by all calls on that GPU.
+namespace {
+constexpr size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+constexpr size_t kScratchBytes =
+    round256(GGK_MOE_MAX_EXPERTS * sizeof(gg_device_problem_desc)) +
+    round256((2 * (GGK_MOE_MAX_EXPERTS + 1) + 2 * GGK_MOE_MAX_EXPERTS + GGK_MOE_HEADER_INTS) * sizeof(int)) +
+    round256(GGK_SCHEDULER_STATE_INTS * sizeof(int));
+static_assert(kScratchBytes <= GG_MOE_NOALLOC_SCRATCH_BYTES, "the stated maximum holds the largest set");
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[GG_MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+// The current device's address of `scratch` (host code never uses the
+// array's name itself: on the host it is a stand-in, not a device address).
+// Found with hipGetSymbolAddress on the first call on each device, with that
+// device current, then kept.  Not exported: the library's own entry point is
+// its only caller.
+extern "C" __attribute__((visibility("hidden"))) hipError_t gg_moe_scratch(void** ptr, size_t* bytes) {
+  if (ptr == nullptr || bytes == nullptr) return hipErrorInvalidValue;
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return st;
+  if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* p = nullptr;
+    st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st != hipSuccess) return st;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
+  *bytes = GG_MOE_NOALLOC_SCRATCH_BYTES;
+  return hipSuccess;
+}
 
 extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts,
                                       int sort_mode, gg_device_problem_desc* d_problems, int* d_offsets,

@@ -16,6 +16,10 @@
 #include <tuple>
 #include <utility>
 
+// The static scratch array of the allocation-free MoE entry point
+// (gg_moe.hip, not exported): its address on the current device and its size.
+extern "C" hipError_t gg_moe_scratch(void** ptr, size_t* bytes);
+
 namespace grouped_gemm {
 namespace {
 
@@ -835,22 +839,28 @@ MoeGroupedGemm& MoeGroupedGemm::operator=(MoeGroupedGemm&& other) noexcept {
   return *this;
 }
 
-// Checks the layout and sizes the device-side set: E descriptors, 2 (E + 1) +
-// 2 E + GGK_MOE_HEADER_INTS ints and the scheduler state, in one allocation
-// (kept from the previous build when large enough).  On any failure the
-// object is reset and run() returns hipErrorInvalidDevicePointer.
-hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode) {
-  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
-  impl_->reset();
+namespace {
+
+// How a MoE group launches: its layout as the kernels read it, the kernel
+// (variant, path), the addressing form and the grid.
+struct MoePlan {
+  ggk_moe_layout layout{};
   RuntimeMode mode;
-  hipError_t status = resolve_runtime_mode(config, &mode);
+  int addressing = GGK_ADDR_32;
+  int grid = 0;
+};
+
+hipError_t plan_moe(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode, MoePlan* plan) {
+  hipError_t status = resolve_runtime_mode(config, &plan->mode);
   if (status != hipSuccess) return status;
+  RuntimeMode& mode = plan->mode;
   const int e = layout.experts;
   const int sm = static_cast<int>(sort_mode);
   if (e < 1 || e > GGK_MOE_MAX_EXPERTS || sm < 0 || sm > 3) return hipErrorInvalidValue;
   if (layout.a == nullptr || layout.b == nullptr || layout.d == nullptr) return hipErrorInvalidDevicePointer;
 
-  ggk_moe_layout L{};
+  ggk_moe_layout& L = plan->layout;
+  L = ggk_moe_layout{};
   L.experts = e;
   L.n = layout.n;
   L.k = layout.k;
@@ -894,34 +904,60 @@ hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& co
     if (status != hipSuccess) return status;
     wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   }
+  plan->addressing = wide == 1 ? GGK_ADDR_64 : GGK_ADDR_32;
 
   OccupancyInfo occupancy{};
   status = cached_occupancy(config, mode, &occupancy);
   if (status != hipSuccess) return status;
+  // The total is known only on the device: one workgroup per resident slot
+  // (or the requested persistent size); idle ones retire at once.
+  plan->grid = config.persistent_ctas > 0
+                   ? config.persistent_ctas
+                   : std::max(1, occupancy.sm_count * std::max(1, occupancy.active_blocks_per_sm));
+  return hipSuccess;
+}
 
-  const size_t ints = 2 * static_cast<size_t>(e + 1) + 2 * static_cast<size_t>(e) + GGK_MOE_HEADER_INTS;
-  const size_t desc_bytes = DeviceBuffer::round256(e * sizeof(DeviceProblemDesc));
-  const size_t int_bytes = DeviceBuffer::round256(ints * sizeof(int));
-  const size_t state_bytes = DeviceBuffer::round256(GGK_SCHEDULER_STATE_INTS * sizeof(int));
-  status = impl_->buffer.reserve(desc_bytes + int_bytes + state_bytes);
+// Byte layout of a MoE group's device-side set of E experts: descriptors,
+// ints (offsets [2 (E + 1)] | permutation [E] | order [E] | header), then the
+// scheduler state, each part on a 256-byte boundary.
+struct MoeBytes {
+  size_t desc, ints, state;
+  size_t total() const { return desc + ints + state; }
+};
+MoeBytes moe_bytes(int experts) {
+  const size_t ints = 2 * static_cast<size_t>(experts + 1) + 2 * static_cast<size_t>(experts) + GGK_MOE_HEADER_INTS;
+  return MoeBytes{DeviceBuffer::round256(experts * sizeof(DeviceProblemDesc)), DeviceBuffer::round256(ints * sizeof(int)),
+                  DeviceBuffer::round256(GGK_SCHEDULER_STATE_INTS * sizeof(int))};
+}
+
+}  // namespace
+
+// Checks the layout and sizes the device-side set: E descriptors, 2 (E + 1) +
+// 2 E + GGK_MOE_HEADER_INTS ints and the scheduler state, in one allocation
+// (kept from the previous build when large enough).  On any failure the
+// object is reset and run() returns hipErrorInvalidDevicePointer.
+hipError_t MoeGroupedGemm::build(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode) {
+  if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
+  impl_->reset();
+  MoePlan plan;
+  hipError_t status = plan_moe(layout, config, sort_mode, &plan);
   if (status != hipSuccess) return status;
-  status = ggk_zero(impl_->buffer.base, desc_bytes + int_bytes + state_bytes);
+  const MoeBytes bytes = moe_bytes(plan.layout.experts);
+  status = impl_->buffer.reserve(bytes.total());
+  if (status != hipSuccess) return status;
+  status = ggk_zero(impl_->buffer.base, bytes.total());
   if (status != hipSuccess) return status;
 
   unsigned char* base = static_cast<unsigned char*>(impl_->buffer.base);
   impl_->d_problems = reinterpret_cast<DeviceProblemDesc*>(base);
-  impl_->d_ints = reinterpret_cast<int*>(base + desc_bytes);
-  impl_->d_state = reinterpret_cast<int*>(base + desc_bytes + int_bytes);
-  impl_->layout = L;
-  impl_->variant = mode.variant;
-  impl_->path = mode.path;
-  impl_->addressing = wide == 1 ? GGK_ADDR_64 : GGK_ADDR_32;
-  impl_->sort_mode = sm;
-  // The total is known only on the device: one workgroup per resident slot
-  // (or the requested persistent size); idle ones retire at once.
-  impl_->grid_ctas = config.persistent_ctas > 0
-                         ? config.persistent_ctas
-                         : std::max(1, occupancy.sm_count * std::max(1, occupancy.active_blocks_per_sm));
+  impl_->d_ints = reinterpret_cast<int*>(base + bytes.desc);
+  impl_->d_state = reinterpret_cast<int*>(base + bytes.desc + bytes.ints);
+  impl_->layout = plan.layout;
+  impl_->variant = plan.mode.variant;
+  impl_->path = plan.mode.path;
+  impl_->addressing = plan.addressing;
+  impl_->sort_mode = static_cast<int>(sort_mode);
+  impl_->grid_ctas = plan.grid;
   return hipSuccess;
 }
 
@@ -952,5 +988,40 @@ const int* MoeGroupedGemm::device_sorted_to_original() const {
 }
 const int* MoeGroupedGemm::device_order() const { return impl_ != nullptr && impl_->d_ints ? impl_->order() : nullptr; }
 const int* MoeGroupedGemm::device_header() const { return impl_ != nullptr && impl_->d_ints ? impl_->header() : nullptr; }
+
+// The allocation-free MoE group: the set MoeGroupedGemm keeps in its own
+// allocation lives in the library's static scratch array of the current
+// device (gg_moe.hip).  The scheduler state is cleared by a fill kernel
+// before the prepare kernel (no memset node, so the sequence can be captured
+// in a graph); the prepare kernel rewrites the rest.
+hipError_t run_moe_grouped_gemm_noalloc(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode,
+                                        const int* d_counts, hipStream_t stream) {
+  MoePlan plan;
+  hipError_t status = plan_moe(layout, config, sort_mode, &plan);
+  if (status != hipSuccess) return status;
+  if (d_counts == nullptr) return hipErrorInvalidDevicePointer;
+  void* scratch = nullptr;
+  size_t capacity = 0;
+  status = gg_moe_scratch(&scratch, &capacity);
+  if (status != hipSuccess) return status;
+  const MoeBytes bytes = moe_bytes(plan.layout.experts);
+  if (bytes.total() > capacity) return hipErrorInvalidValue;
+  unsigned char* base = static_cast<unsigned char*>(scratch);
+  auto* problems = reinterpret_cast<DeviceProblemDesc*>(base);
+  int* ints = reinterpret_cast<int*>(base + bytes.desc);
+  int* state = reinterpret_cast<int*>(base + bytes.desc + bytes.ints);
+  const int e = plan.layout.experts;
+  int* perm = ints + 2 * (e + 1);
+  int* order = perm + e;
+  int* header = order + e;
+  // 0.0f is the all-zero bit pattern.
+  status = ggk_fill_f32(reinterpret_cast<float*>(state), GGK_SCHEDULER_STATE_INTS, 0.0f, stream);
+  if (status != hipSuccess) return status;
+  status = ggk_moe_prepare(plan.mode.variant, plan.mode.path, &plan.layout, d_counts, static_cast<int>(sort_mode),
+                           problems, ints, perm, order, header, stream);
+  if (status != hipSuccess) return status;
+  return ggk_launch_grouped_device(plan.mode.variant, plan.mode.path, plan.addressing, problems, ints + e + 1, order, e,
+                                   header, state, plan.grid, stream);
+}
 
 }  // namespace grouped_gemm

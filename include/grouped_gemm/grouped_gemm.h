@@ -255,4 +255,11 @@ class MoeGroupedGemm {
   Impl* impl_;
 };
 
+// Allocation-free form of MoeGroupedGemm (build + run + destroy in one call),
+// for callers that cannot allocate device memory; no counterpart in the
+// reference.  See gg_moe_run_noalloc (grouped_gemm_amd.h) for the limits and
+// the rule that calls on one GPU must not overlap.
+hipError_t run_moe_grouped_gemm_noalloc(const MoeLayout& layout, const KernelConfig& config, SortMode sort_mode,
+                                        const int* d_counts, hipStream_t stream = nullptr);
+
 }  // namespace grouped_gemm

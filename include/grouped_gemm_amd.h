@@ -159,6 +159,23 @@ int gg_moe_device_buffers(const gg_moe* moe, const gg_device_problem_desc** prob
                           const int** sorted_to_original, const int** header, const int** order);
 void gg_moe_destroy(gg_moe* moe);
 
+/* Allocation-free MoE group.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  The same result as
+ * gg_moe_create(layout, config, sort_mode), gg_moe_run(d_counts, stream) and
+ * gg_moe_destroy, with the prepared set and the scheduler state in a static
+ * device array of GG_MOE_NOALLOC_SCRATCH_BYTES per GPU (held until the
+ * process ends) instead of an allocation: nothing is allocated or freed and
+ * the host does not wait.  At most GGK_MOE_MAX_EXPERTS experts (more is
+ * hipErrorInvalidValue).  Every call on a GPU uses that GPU's one array, which
+ * keeps the last call's contents: each call clears the scheduler state
+ * itself, and calls that overlap on one GPU (on different streams, or from
+ * different threads without stream order between them) race and give wrong
+ * results; calls in one stream's order do not overlap. */
+#define GG_MOE_NOALLOC_SCRATCH_BYTES 99840
+int gg_moe_run_noalloc(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode,
+                       const int* d_counts, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

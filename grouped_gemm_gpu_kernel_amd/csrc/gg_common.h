@@ -147,6 +147,7 @@ template <int V, int PATH> struct KernelShape;
 #ifndef GG_DMA_BUFFERS
 #define GG_DMA_BUFFERS 0  // 0: see KernelShape::BUFFERS
 #endif
+
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   // The GG_* shape macros retune the 128x64x32 variant only.
   static constexpr bool kTuned = V == GGK_VARIANT_128x64x32;
@@ -655,6 +656,14 @@ struct DmaLoader {
   // and B rows at k >= K become zero, and the matrices' last values are put
   // back where a straddling dword read them as zero.
   __device__ __forceinline__ void fix_last_stage(int kt, uint16_t* stage) const {
+    // The inputs pass through empty asm statements: everything computed from
+    // them stays inside the caller's branch (computed early, the masks below
+    // would cost vector instructions and registers in every k-step, though
+    // only one stage per tile needs them).
+    int k = this->k, m = this->m, n = this->n, a_row = this->a_row, b_row = this->b_row;
+    int a_col8 = this->a_col8, b_col8 = this->b_col8, m0 = this->m0, n0 = this->n0;
+    asm volatile("" : "+s"(k), "+s"(m), "+s"(n), "+s"(m0), "+s"(n0), "+s"(kt));
+    asm volatile("" : "+v"(a_row), "+v"(b_row), "+v"(a_col8), "+v"(b_col8));
     const int lane = opaque_tid() & (kWave - 1);
 #pragma unroll
     for (int i = 0; i < NA; ++i) {

@@ -187,6 +187,25 @@ __device__ __forceinline__ int work_tiles_n(const gg_device_problem_desc& p) {
   return (p.tiles_n + TN - 1) / TN;
 }
 
+// Position (wm, wn) of work tile `local` of a problem with wtm x wtn work
+// tiles, in the order the grouped kernel meets them: groups of kGroupRows rows
+// (fewer in the last group), column by column within a group, row by row
+// within a column.  Any run of consecutive tiles then covers a block a few
+// rows tall, so the workgroups of one XCD, which claim consecutive indices,
+// share A row panels and B column panels in that XCD's L2 (32 tiles touch 12
+// panels instead of 33 for a long row).  A bijection of [0, wtm * wtn): it
+// decides only the order, and every tile is computed the same way.
+constexpr int kGroupRows = 4;
+__device__ __forceinline__ void work_tile_position(int local, int wtm, int wtn, int& wm, int& wn) {
+  const int group_size = kGroupRows * wtn;
+  const int group = local / group_size;
+  const int first = group * kGroupRows;
+  const int rows = wtm - first < kGroupRows ? wtm - first : kGroupRows;
+  const int within = local - group * group_size;
+  wn = within / rows;
+  wm = first + (within - wn * rows);
+}
+
 // At least KernelShape::WAVES_PER_EU waves per SIMD: 2 allows 256 VGPRs +
 // AGPRs per lane (a 512-thread workgroup, or two 256-thread ones), 1 allows 512.
 #define GG_KERNEL_ATTRS(V, PATH)                          \
@@ -264,27 +283,26 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
     // Uniform index into read-only memory: scalar loads of the 80-byte descriptor.
     const gg_device_problem_desc p = load_problem(args.problems, prob);
     const int wtn = work_tiles_n<S::TM, S::TN>(p);
-    if (wtn > 0) {
-      const int wm = local / wtn;
-      const int wn = local - wm * wtn;
-      if (wm * S::TM < p.tiles_m) {
-        if (TRACED && args.tile_map != nullptr) {
-          // Record every reference tile this work tile covers under its
-          // reference index.
-          const int base = ((const_int_ptr)args.tile_offsets)[prob];
-          if (tid < S::TM * S::TN) {
-            const int tm = wm * S::TM + tid / S::TN;
-            const int tn = wn * S::TN + tid % S::TN;
-            if (tm < p.tiles_m && tn < p.tiles_n) {
-              const int ref = base + tm * p.tiles_n + tn;
-              args.tile_map[3 * ref + 0] = prob;
-              args.tile_map[3 * ref + 1] = tm;
-              args.tile_map[3 * ref + 2] = tn;
-            }
+    const int wtm = (p.tiles_m + S::TM - 1) / S::TM;
+    if (wtn > 0 && wtm > 0 && local < wtm * wtn) {
+      int wm, wn;
+      work_tile_position(local, wtm, wtn, wm, wn);
+      if (TRACED && args.tile_map != nullptr) {
+        // Record every reference tile this work tile covers under its
+        // reference index.
+        const int base = ((const_int_ptr)args.tile_offsets)[prob];
+        if (tid < S::TM * S::TN) {
+          const int tm = wm * S::TM + tid / S::TN;
+          const int tn = wn * S::TN + tid % S::TN;
+          if (tm < p.tiles_m && tn < p.tiles_n) {
+            const int ref = base + tm * p.tiles_n + tn;
+            args.tile_map[3 * ref + 0] = prob;
+            args.tile_map[3 * ref + 1] = tm;
+            args.tile_map[3 * ref + 2] = tn;
           }
-        } else {
-          Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
         }
+      } else {
+        Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
       }
     }
     if (!asked) request();

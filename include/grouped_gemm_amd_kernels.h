@@ -154,9 +154,14 @@ hipError_t ggk_device_info_get(ggk_device_info* out);
  * variant's macro-tiles (src/grouped_gemm.cu:54-65) with `threads` threads;
  * rows = tiles_m * cta_m, and stage_k is the depth of one LDS stage.
  * The work-tile count of a problem is ceil(tiles_m_p / tiles_m) *
- * ceil(tiles_n_p / tiles_n), numbered row-major; the reference tile (tm, tn)
- * belongs to work tile (tm / tiles_m, tn / tiles_n).  No reference
- * counterpart: the reference computes one macro-tile per CTA. */
+ * ceil(tiles_n_p / tiles_n); the reference tile (tm, tn) belongs to work
+ * tile (wm, wn) = (tm / tiles_m, tn / tiles_n).  The grouped kernel numbers a
+ * problem's work tiles in groups of 4 work-tile rows, column by column within
+ * a group (index = first row of the group * wn_count + column * rows in the
+ * group + row within the group), so that the work tiles in flight at once
+ * share A and B panels; the single-problem kernel numbers them row-major.
+ * No reference counterpart: the reference computes one macro-tile per CTA
+ * and numbers tiles row-major. */
 typedef struct ggk_work_shape {
   int tiles_m;
   int tiles_n;
@@ -192,7 +197,7 @@ int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* proble
  * for equal counts) splits the work-tile indices into the per-XCD chunks.
  * d_work_table[2 * total_work] (device memory, or NULL) holds for each
  * work-tile index the problem (in sorted order) and the work tile's index
- * within that problem (row-major), which the kernel then reads instead of
+ * within that problem (numbered as described at ggk_work_shape), which the kernel then reads instead of
  * searching d_work_offsets for them.  grid workgroups claim work tiles until
  * total_work are done. */
 hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,

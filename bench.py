@@ -32,8 +32,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--clock-warmup", type=float, default=0.3,
                     help="seconds of untimed launches before the first timed mode (0.1 s before the others)")
-    ap.add_argument("--workload", default="mixed512",
-                    choices=["plumbing16", "mixed512", "dense64", "moe64", "longtail4096"])
+    ap.add_argument("--workload", default=None,
+                    choices=["plumbing16", "mixed512", "dense64", "moe64", "longtail4096"],
+                    help="default mixed512 (summaries: the workload profiled, for useful-work ratios)")
     ap.add_argument("--config", default=None, help="macro-tile, default: the workload's")
     ap.add_argument("--modes", default="0,1,2,3", help="sort modes to time")
     ap.add_argument("--no-baseline", action="store_true", help="skip the per-problem-launch baseline")
@@ -48,10 +49,26 @@ def parse_args():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB a few times (for scaling HBM "
                          "byte counters of a profiler run) and exit")
+    ap.add_argument("--no-moe-device", action="store_true", help="skip the device-side MoE prepare timing")
     ap.add_argument("--profile-summary", nargs="+", metavar="DIR",
                     help="only summarize rocprofv3 CSV output folders (kernel trace and/or counters) and exit")
-    ap.add_argument("--kernel", default="gg_grouped_kernel", help="kernel-name filter for --profile-summary")
-    return ap.parse_args()
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="only turn FETCH_SIZE / WRITE_SIZE folders of the grouped kernel and of a "
+                         "--calibrate-copy run into HBM bytes per launch of --workload and exit")
+    ap.add_argument("--copy-mib", type=int, default=256, help="size of the --calibrate-copy run summarized")
+    ap.add_argument("--kernel", default=r"gg_grouped_kernel<\d+,\s*\d+,\s*false",
+                    help="kernel-name regex for the summaries (default: the untraced grouped kernel)")
+    ap.add_argument("--modes-of-segments", default="",
+                    help="summaries: comma-separated sort-mode names of the profiled bench run, in its "
+                         "order: dispatches are reported per mode (the bench makes a traced dispatch "
+                         "after each mode's timed runs)")
+    ap.add_argument("--last", type=int, default=0,
+                    help="summaries: count only the last N dispatches of each mode (its --steps)")
+    args = ap.parse_args()
+    args.workload_given = args.workload is not None
+    if args.workload is None:
+        args.workload = "mixed512"
+    return args
 
 
 def calibrate_copy(torch, mib: int) -> int:
@@ -285,41 +302,153 @@ def _csv_rows(path: Path):
         return list(csv.DictReader(f))
 
 
-def profile_summary(dirs, kernel_filter: str) -> int:
-    """Prints what a rocprofv3 --output-format csv folder holds for kernels matching kernel_filter:
-    dispatch count and mean/min/max duration (kernel trace), mean counter value per dispatch
-    (counter collection)."""
+TRACED_KERNEL = r"gg_grouped_kernel<\d+,\s*\d+,\s*true"
+
+
+def _dispatches(d: Path):
+    """[(dispatch id, kernel name, {"duration_us" or counter: value})] from the rocprofv3 CSV output
+    under d (kernel traces and counter collections), in dispatch order; a counter's rows of one
+    dispatch are summed."""
+    per = {}
+    for trace in sorted(d.rglob("*kernel_trace.csv")):
+        for r in _csv_rows(trace):
+            e = per.setdefault(int(r["Dispatch_Id"]), (r["Kernel_Name"], {}))
+            e[1]["duration_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    for cc in sorted(d.rglob("*counter_collection.csv")):
+        for r in _csv_rows(cc):
+            e = per.setdefault(int(r["Dispatch_Id"]), (r["Kernel_Name"], {}))
+            e[1][r["Counter_Name"]] = e[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [(i, per[i][0], per[i][1]) for i in sorted(per)]
+
+
+def _segments(dispatches, kernel_filter: str, names, last: int):
+    """{(kernel, segment name): {metric: [values]}} for the kernels matching kernel_filter.  With
+    names, the dispatches are cut into segments at each traced grouped-kernel dispatch (bench.py
+    makes one after each sort mode's timed runs, so segment i holds mode i's clock warm-up, warm-up
+    and timed runs) and only the last `last` dispatches of each segment count (0: all of them);
+    dispatches after the last cut form a segment named "after".  Without names: one segment "all"."""
     import re
-    pat = re.compile(kernel_filter)
+    pat, cut = re.compile(kernel_filter), re.compile(TRACED_KERNEL)
+    segs, current, seg = {}, {}, 0
+
+    def close(name):
+        for kname, rows in current.items():
+            rows = rows[-last:] if last > 0 else rows
+            out = segs.setdefault((kname, name), {})
+            for metrics in rows:
+                for key, v in metrics.items():
+                    out.setdefault(key, []).append(v)
+
+    for _, kname, metrics in dispatches:
+        if names and cut.search(kname):
+            close(names[seg] if seg < len(names) else f"segment{seg}")
+            current, seg = {}, seg + 1
+        elif pat.search(kname):
+            current.setdefault(kname, []).append(metrics)
+    close("after" if names else "all")
+    return segs
+
+
+def _stats(v) -> str:
+    return f"dispatches {len(v)}  mean {sum(v) / len(v):.6g}  min {min(v):.6g}  max {max(v):.6g}"
+
+
+MFMA_CYCLES = 32        # v_mfma_f32_32x32x16_f16: cycles a SIMD is busy per instruction
+MFMA_MACS = 32 * 32 * 16
+SIMDS_PER_CU = 4
+XCDS = 8
+
+
+def _derived(metrics, workload) -> list:
+    """Ratios of the counters of one sort mode (means per dispatch):
+      mfma_busy        SQ_VALU_MFMA_BUSY_CYCLES / (4 SIMDs x SQ_BUSY_CU_CYCLES): share of the SIMD
+                       cycles of busy CUs spent in MFMA;
+      mfma_executed    SQ_VALU_MFMA_BUSY_CYCLES / 32 cycles per 32x32x16 MFMA, against the
+                       workload's useful MFMAs (sum m n k / 16384): padding of partial tiles;
+      l2_hit           TCC_HIT / (TCC_HIT + TCC_MISS);
+      lds_bank_conflict  SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (cycles);
+      clock_ghz        GRBM_GUI_ACTIVE / 8 XCDs / the dispatch's duration (when traced)."""
+    mean = {k: sum(v) / len(v) for k, v in metrics.items()}
+    out = []
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
+        out.append(f"mfma_busy: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (SIMDS_PER_CU * mean['SQ_BUSY_CU_CYCLES']):.4f}")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and workload:
+        from grouped_gemm_gpu_kernel_amd.workloads import make_spec
+        useful = make_spec(workload).flops() / 2 / MFMA_MACS
+        executed = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / MFMA_CYCLES
+        out.append(f"mfma_executed: {executed:.6g} useful: {useful:.6g} ratio: {executed / useful:.4f}")
+    if "TCC_HIT_sum" in mean and "TCC_MISS_sum" in mean:
+        tot = mean["TCC_HIT_sum"] + mean["TCC_MISS_sum"]
+        if tot > 0:
+            out.append(f"l2_hit: {mean['TCC_HIT_sum'] / tot:.4f}")
+    if "SQ_LDS_BANK_CONFLICT" in mean and mean.get("SQ_LDS_IDX_ACTIVE"):
+        out.append(f"lds_bank_conflict: {mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_LDS_IDX_ACTIVE']:.4f}")
+    if "GRBM_GUI_ACTIVE" in mean and mean.get("duration_us"):
+        out.append(f"clock_ghz: {mean['GRBM_GUI_ACTIVE'] / XCDS / (mean['duration_us'] * 1e3):.3f}")
+    return out
+
+
+def profile_summary(dirs, kernel_filter: str, names=(), last: int = 0, workload=None) -> int:
+    """Prints what rocprofv3 --output-format csv folders hold for kernels matching kernel_filter:
+    per dispatch, mean/min/max of the duration in us (kernel trace) and of each counter (counter
+    collection), per sort mode when the mode names are given (see _segments), and the ratios of
+    _derived (useful MFMAs from `workload`)."""
     for d in dirs:
         d = Path(d)
         print(f"== {d}")
-        for trace in sorted(d.rglob("*kernel_trace.csv")):
-            groups = {}
-            for r in _csv_rows(trace):
-                name = r.get("Kernel_Name", "")
-                if not pat.search(name):
-                    continue
-                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # us
-                groups.setdefault(name, []).append(dur)
-            for name, durs in groups.items():
-                print(f"kernel {name}")
-                print(f"  dispatches {len(durs)}  mean_us {sum(durs) / len(durs):.2f}  "
-                      f"min_us {min(durs):.2f}  max_us {max(durs):.2f}")
-                print(f"  durations_us {' '.join(f'{x:.1f}' for x in durs)}")
-        for cc in sorted(d.rglob("*counter_collection.csv")):
-            per = {}
-            for r in _csv_rows(cc):
-                name = r.get("Kernel_Name", "")
-                if not pat.search(name):
-                    continue
-                per.setdefault((name, r["Counter_Name"]), {}).setdefault(r["Dispatch_Id"], 0.0)
-                per[(name, r["Counter_Name"])][r["Dispatch_Id"]] += float(r["Counter_Value"])
-            for (name, counter), vals in per.items():
-                v = list(vals.values())
-                print(f"counter {counter} kernel {name}")
-                print(f"  dispatches {len(v)}  mean_per_dispatch {sum(v) / len(v):.6g}  "
-                      f"min {min(v):.6g}  max {max(v):.6g}")
+        for (kname, seg), metrics in _segments(_dispatches(d), kernel_filter, names, last).items():
+            for key, v in sorted(metrics.items()):
+                print(f"{kname} [{seg}] {key}: {_stats(v)}")
+            for line in _derived(metrics, workload):
+                print(f"{kname} [{seg}] {line}")
+    return 0
+
+
+def traffic_summary(dirs, copy_mib: int, workload: str, kernel_filter: str, names, last: int) -> int:
+    """HBM bytes per launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each divided by what
+    the same counter reads per byte of a plain device-to-device copy of copy_mib MiB (the copy reads
+    and writes copy_mib MiB once), per sort mode.  Prints the lines of a
+    profiles/gg_grouped_kernel_<workload>_hbm_traffic.txt file."""
+    from grouped_gemm_gpu_kernel_amd.workloads import make_spec
+
+    fetch_dir, write_dir, copy_fetch_dir, copy_write_dir = (Path(x) for x in dirs)
+    copy_bytes = copy_mib << 20
+
+    def copy_reading(d, counter):
+        segs = _segments(_dispatches(d), "copyBuffer", (), 0)
+        vals = [v for m in segs.values() for v in m.get(counter, [])]
+        if not vals:
+            raise SystemExit(f"{d}: no copyBuffer dispatch with {counter}")
+        return sum(vals) / len(vals), len(vals)
+
+    cf, ncf = copy_reading(copy_fetch_dir, "FETCH_SIZE")
+    cw, ncw = copy_reading(copy_write_dir, "WRITE_SIZE")
+    fetch_scale = cf * 1024 / copy_bytes
+    write_scale = cw * 1024 / copy_bytes
+    fsegs = _segments(_dispatches(fetch_dir), kernel_filter, names, last)
+    wsegs = _segments(_dispatches(write_dir), kernel_filter, names, last)
+    algo = make_spec(workload).algorithmic_bytes()
+    print(f"# copy calibration, {copy_mib} MiB read + {copy_mib} MiB written per dispatch: FETCH_SIZE "
+          f"{cf:.0f} KiB ({ncf} dispatches) -> fetch_scale {fetch_scale:.4f}; WRITE_SIZE {cw:.0f} KiB "
+          f"({ncw} dispatches) -> write_scale {write_scale:.4f}")
+    print("# traffic = FETCH_SIZE * 1024 / fetch_scale + WRITE_SIZE * 1024 / write_scale, bytes per launch")
+    print(f"algorithmic_bytes: {algo:.0f}")
+    print(f"fetch_scale: {fetch_scale:.4f}")
+    print(f"write_scale: {write_scale:.4f}")
+    for (kname, seg), fm in fsegs.items():
+        wm = wsegs.get((kname, seg), {})
+        if "FETCH_SIZE" not in fm or "WRITE_SIZE" not in wm:
+            continue
+        fv, wv = fm["FETCH_SIZE"], wm["WRITE_SIZE"]
+        fb = sum(fv) / len(fv) * 1024 / fetch_scale
+        wb = sum(wv) / len(wv) * 1024 / write_scale
+        print(f"# {seg}: {kname}")
+        print(f"#   FETCH_SIZE KiB {_stats(fv)}")
+        print(f"#   WRITE_SIZE KiB {_stats(wv)}")
+        print(f"fetch_bytes_per_launch {seg}: {fb:.0f}")
+        print(f"write_bytes_per_launch {seg}: {wb:.0f}")
+        print(f"traffic_bytes_per_launch {seg}: {fb + wb:.0f}")
+        print(f"traffic_over_algorithmic {seg}: {(fb + wb) / algo:.3f}")
     return 0
 
 
@@ -344,8 +473,12 @@ def committed_traffic(workload: str, mode: str):
 
 def main() -> int:
     args = parse_args()
+    names = [x for x in args.modes_of_segments.split(",") if x]
     if args.profile_summary:
-        return profile_summary(args.profile_summary, args.kernel)
+        return profile_summary(args.profile_summary, args.kernel, names, args.last,
+                               args.workload if args.workload_given else None)
+    if args.traffic_summary:
+        return traffic_summary(args.traffic_summary, args.copy_mib, args.workload, args.kernel, names, args.last)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the grouped GEMM shards "
               "problems across GPUs with no exchange step, see the design notes.", file=sys.stderr)
@@ -404,9 +537,11 @@ def main() -> int:
     timed = []
     for i, (mode, prep, ex, prep_ms) in enumerate(built):
         clock_warmup(ex, args.clock_warmup if i == 0 else min(args.clock_warmup, 0.1))
-        timed.append(time_runs(torch, lambda: ex.run(stream), args.steps, args.warmup))
-    for (mode, prep, ex, prep_ms), ms in zip(built, timed):
-        tail_idle = measured_tail_idle(torch, ex)
+        ms = time_runs(torch, lambda: ex.run(stream), args.steps, args.warmup)
+        # The traced run right after a mode's timed runs also marks, in a profiler's dispatch list,
+        # where that mode's runs end (--profile-summary / --traffic-summary --modes-of-segments).
+        timed.append((ms, measured_tail_idle(torch, ex)))
+    for (mode, prep, ex, prep_ms), (ms, tail_idle) in zip(built, timed):
         row = {
             "mode": api.sort_mode_name(mode), "prep_ms": round(prep_ms, 3), "kernel_ms": round(ms, 4),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "tiles": prep.total_tiles,
@@ -429,7 +564,7 @@ def main() -> int:
         print(f"# {baseline}", file=sys.stderr, flush=True)
 
     best_mode = next(m for m in modes if api.sort_mode_name(m) == best[0]["mode"])
-    moe_device = None if args.fma else moe_device_prepare(torch, dw, spec, cfg, best_mode, stream, args.steps,
+    moe_device = None if (args.fma or args.no_moe_device) else moe_device_prepare(torch, dw, spec, cfg, best_mode, stream, args.steps,
                                                           args.warmup)
     vendor_rows = None if (args.no_vendor or args.fma) else vendor_baseline(spec, config_name, int(best_mode),
                                                                             args.steps, args.warmup)

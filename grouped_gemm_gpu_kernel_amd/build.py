@@ -111,7 +111,7 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), c
 
     def compile_host(name: str) -> Path:
         obj = build_dir / (Path(name).stem + ".o")
-        _run([*CXX_FLAGS, f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)])
+        _run([*CXX_FLAGS, *extra, f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)])
         return obj
 
     with ThreadPoolExecutor(max_workers=4) as pool:

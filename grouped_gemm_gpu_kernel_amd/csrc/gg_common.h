@@ -147,6 +147,9 @@ template <int V, int PATH> struct KernelShape;
 #ifndef GG_DMA_BUFFERS
 #define GG_DMA_BUFFERS 0  // 0: see KernelShape::BUFFERS
 #endif
+#ifndef GG_TILE_CLASSES
+#define GG_TILE_CLASSES 1  // 0: every work tile in the full 256 x 256 form
+#endif
 
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   // The GG_* shape macros retune the 128x64x32 variant only.
@@ -173,12 +176,26 @@ template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   // 256 x 256 work tile's still spills: launches route that form to the
   // 128 x 128 work tile of the same macro-tile).
   using G = Geometry<BM, BN, GG_STAGE_K, 2, THREADS, BUFFERS, true>;
+  // Edge classes of the 256 x 256 work tile (32-bit addressing form): a work
+  // tile with at most BM / 2 rows or BN / 2 columns inside the problem stages
+  // only that half of A or B, so a stage is 48 KB (32 KB when both) and three
+  // (four) LDS buffers fit -- two (three) stages in flight instead of one,
+  // which is what a tile that streams its operands from HBM is bound by.  The
+  // same 512 threads compute it in 64 x 64 (32 x 64) wave blocks; every D
+  // element is still one lane's 32x32x16 MFMA chain over ascending k with the
+  // same epilogue, so D does not depend on the class.
+  static constexpr bool CLASSES = GG_TILE_CLASSES != 0 && kTuned && BM == 256 && BN == 256 && THREADS == 512;
+  using GR = Geometry<BM / 2, BN, GG_STAGE_K, 2, THREADS, 3, true>;       // rows <= BM / 2
+  using GC = Geometry<BM, BN / 2, GG_STAGE_K, 2, THREADS, 3, true>;       // columns <= BN / 2
+  using GRC = Geometry<BM / 2, BN / 2, GG_STAGE_K, 2, THREADS, 4, true>;  // both
+  static constexpr int WAVE_M_R = 64, WAVE_M_C = 64, WAVE_M_RC = 32;
 };
 template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr int TM = 1;
   static constexpr int TN = 1;
   static constexpr int WAVES_PER_EU = 2;
   using G = Geometry<VariantTile<V>::M, VariantTile<V>::N, GG_STAGE_K, GG_STAGE_DEPTH, 256>;
+  static constexpr bool CLASSES = false;
 };
 
 // threadIdx.x behind an empty asm: the compiler must assume it changes at

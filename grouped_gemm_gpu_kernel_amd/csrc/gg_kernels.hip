@@ -195,7 +195,10 @@ __device__ __forceinline__ int work_tiles_n(const gg_device_problem_desc& p) {
 // share A row panels and B column panels in that XCD's L2 (32 tiles touch 12
 // panels instead of 33 for a long row).  A bijection of [0, wtm * wtn): it
 // decides only the order, and every tile is computed the same way.
-constexpr int kGroupRows = 4;
+#ifndef GG_GROUP_ROWS
+#define GG_GROUP_ROWS 4
+#endif
+constexpr int kGroupRows = GG_GROUP_ROWS;
 __device__ __forceinline__ void work_tile_position(int local, int wtm, int wtn, int& wm, int& wn) {
   const int group_size = kGroupRows * wtn;
   const int group = local / group_size;
@@ -216,8 +219,7 @@ template <int V, int PATH, bool TRACED, bool WIDE>
 __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
   using S = KernelShape<V, PATH>;
   using G = typename S::G;
-  using Tile = typename TileFor<S, PATH>::type;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[KernelLds<S>::HALVES];
   __shared__ int s_claim[2];
   __shared__ int s_schedule[kChunks + 2];
 
@@ -302,7 +304,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
           }
         }
       } else {
-        Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
+        run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
       }
     }
     if (!asked) request();
@@ -347,15 +349,14 @@ template <int V, int PATH, bool WIDE>
 __global__ GG_KERNEL_ATTRS(V, PATH) void gg_single_kernel(gg_device_problem_desc p) {
   using S = KernelShape<V, PATH>;
   using G = typename S::G;
-  using Tile = typename TileFor<S, PATH>::type;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[G::LDS_HALVES];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[KernelLds<S>::HALVES];
   const int t = blockIdx.x;
   const int wtn = work_tiles_n<S::TM, S::TN>(p);
   const int wtm = (p.tiles_m + S::TM - 1) / S::TM;
   if (wtn <= 0 || t >= wtm * wtn) return;
   const int wm = t / wtn;
   const int wn = t - wm * wtn;
-  Tile::template run<WIDE>(p, wm * G::BM, wn * G::BN, lds, [] { return false; });
+  run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, [] { return false; });
 }
 
 // ---------------------------------------------------------------------------

@@ -309,7 +309,12 @@ struct MfmaTile {
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
                 const int fm = chunk * EPI_ROWS + i;
-                const uint32_t off = 4u * ((uint32_t)(fm * 32 + 8 * g + lrow) * (uint32_t)p.ldc + fn * 32 + lcol);
+                // Vectors wholly past N would read the next row's head (inside
+                // the resource) for nothing: they take an offset past it.
+                const bool in_n = c0 + fn * 32 + lcol < p.n;
+                const uint32_t off =
+                    in_n ? 4u * ((uint32_t)(fm * 32 + 8 * g + lrow) * (uint32_t)p.ldc + fn * 32 + lcol)
+                         : DmaLoader<G>::kOutOfRange;
                 dst[i][fn][g] = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(crs, (int)off, 0, 0));
               }
         } else {
@@ -487,5 +492,45 @@ struct FmaTile {
 template <class S, int PATH> struct TileFor;
 template <class S> struct TileFor<S, GGK_PATH_MFMA> { using type = MfmaTile<typename S::G, S::WAVE_M>; };
 template <class S> struct TileFor<S, GGK_PATH_FMA> { using type = FmaTile<typename S::G>; };
+
+// LDS (binary16 values) a kernel of shape S needs: the largest stage ring of
+// the forms its work tiles take.
+template <class S, bool CLASSES = S::CLASSES>
+struct KernelLds {
+  static constexpr int HALVES = S::G::LDS_HALVES;
+};
+template <class S>
+struct KernelLds<S, true> {
+  static constexpr int a = S::G::LDS_HALVES, r = S::GR::LDS_HALVES, c = S::GC::LDS_HALVES, rc = S::GRC::LDS_HALVES;
+  static constexpr int ab = a > r ? a : r;
+  static constexpr int cd = c > rc ? c : rc;
+  static constexpr int HALVES = ab > cd ? ab : cd;
+  static_assert(2 * HALVES <= 150 * 1024, "the stage rings and the scheduler's words fit the 160 KB of LDS");
+};
+
+// Computes the work tile at (m0, n0): in the edge class its extent inside the
+// problem selects (KernelShape::CLASSES), else in the kernel's own form.  The
+// class is uniform across the workgroup (scalar descriptor and origin).
+template <class S, int PATH, bool WIDE, class OnStart>
+__device__ __forceinline__ void run_work_tile(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
+                                              OnStart&& on_start) {
+  if constexpr (PATH == GGK_PATH_MFMA && !WIDE && S::CLASSES) {
+    const bool rows = p.m - m0 <= S::G::BM / 2;
+    const bool cols = p.n - n0 <= S::G::BN / 2;
+    // The full form first: its code then follows the dispatch as it would
+    // without the edge classes.
+    if (__builtin_expect(!rows && !cols, 1)) {
+      TileFor<S, PATH>::type::template run<false>(p, m0, n0, lds, on_start);
+    } else if (!cols) {
+      MfmaTile<typename S::GR, S::WAVE_M_R>::template run<false>(p, m0, n0, lds, on_start);
+    } else if (!rows) {
+      MfmaTile<typename S::GC, S::WAVE_M_C>::template run<false>(p, m0, n0, lds, on_start);
+    } else {
+      MfmaTile<typename S::GRC, S::WAVE_M_RC>::template run<false>(p, m0, n0, lds, on_start);
+    }
+  } else {
+    TileFor<S, PATH>::type::template run<WIDE>(p, m0, n0, lds, on_start);
+  }
+}
 
 }  // namespace gg

@@ -20,6 +20,12 @@
 // (gg_moe.hip, not exported): its address on the current device and its size.
 extern "C" hipError_t gg_moe_scratch(void** ptr, size_t* bytes);
 
+// 128 x 128 work tiles per CU at or below which a 128x64x32 / 64x128x32 set
+// runs on the small-set variant.
+#ifndef GG_SMALL_SET_TILES_PER_CU
+#define GG_SMALL_SET_TILES_PER_CU 4
+#endif
+
 namespace grouped_gemm {
 namespace {
 
@@ -585,7 +591,7 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
       work += static_cast<int64_t>(ceil_div(ceil_div(p.m, config.cta_m), small.tiles_m)) *
               ceil_div(ceil_div(p.n, config.cta_n), small.tiles_n);
     }
-    if (work <= 4 * static_cast<int64_t>(mode.device.compute_units)) {
+    if (work <= GG_SMALL_SET_TILES_PER_CU * static_cast<int64_t>(mode.device.compute_units)) {
       mode.variant = small_variant;
       mode.work = small;
     }

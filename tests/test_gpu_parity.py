@@ -600,6 +600,68 @@ def test_small_set_work_tiles_bit_identical(torch, config):
         assert np.abs(got - want).max() <= tolerance(p.k, 1.0, 1.0, 1.0, p.alpha, p.beta), i
 
 
+def test_edge_class_work_tiles_bit_identical(torch):
+    """Work tiles with at most 128 rows and/or 128 columns inside their problem run in the edge
+    classes of the 256 x 256 work tile (half-height / half-width stages, more buffers, other wave
+    blocks).  A problem that is a row and/or column prefix of a larger one (same A, B and C memory)
+    must give exactly the larger problem's bits there: every D element is the same MFMA chain over
+    ascending k, whichever class computes it.  Prefixes end inside the first and the second 256-row
+    (column) block and on the 128 boundary; K is 64, odd (2-byte aligned rows, a repaired last
+    stage) and several stages deep.  A filler problem keeps the launch on the 256 x 256 kernel
+    (grid = one workgroup per CU).  The per-problem baseline must give the same bits, and the
+    smallest prefix matches the oracle."""
+    cfg = KernelConfig.named("128x64x32")
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    full = 512
+    prefixes = [(100, 512), (512, 100), (100, 100), (356, 512), (512, 356), (356, 356), (128, 128), (129, 129),
+                (1, 1), (130, 300)]
+    filler_a = torch.rand(4096 * 16, device=dev, generator=g).half()
+    filler_b = torch.rand(16 * 4096, device=dev, generator=g).half()
+    filler_d = torch.empty(4096 * 4096, device=dev)
+    for k in (64, 333, 1000):
+        say(f"edge classes, K = {k}")
+        a = (torch.rand(full * k, device=dev, generator=g) * 2 - 1).half()
+        b = (torch.rand(k * full, device=dev, generator=g) * 2 - 1).half()
+        c = torch.rand(full * full, device=dev, generator=g) * 2 - 1
+        ds = [torch.full((full * full,), float("nan"), device=dev) for _ in range(len(prefixes) + 1)]
+        shapes = [(full, full)] + prefixes
+        probs = [ProblemDesc(m, n, k, a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), k, full, full, full,
+                             1.25, 0.5) for (m, n), d in zip(shapes, ds)]
+        probs.append(ProblemDesc(4096, 4096, 16, filler_a.data_ptr(), filler_b.data_ptr(), None, filler_d.data_ptr(),
+                                 16, 4096, 4096, 4096))
+        ex = GroupedGemmExecutor()
+        assert ex.build(api.prepare_problem_set(probs, cfg, SortMode.kByK), cfg) == 0
+        assert ex.grid_ctas() == 256, "expected the 256 x 256 work-tile kernel"
+        assert ex.run() == 0
+        torch.cuda.synchronize()
+        ex.close()
+        ref = ds[0].view(full, full).view(torch.int32)
+        for (m, n), d in zip(prefixes, ds[1:]):
+            got = d.view(full, full)
+            assert not torch.isnan(got[:m, :n]).any(), (m, n, k)
+            assert torch.equal(got[:m, :n].view(torch.int32), ref[:m, :n]), f"prefix {m} x {n}, K {k}"
+            assert torch.isnan(got[m:, :]).all() and torch.isnan(got[:, n:]).all(), (m, n, k)
+        grouped = [d.clone() for d in ds]
+        for d in ds:
+            d.fill_(float("nan"))
+        assert api.run_baseline_per_problem(probs, cfg) == 0
+        torch.cuda.synchronize()
+        for d0, d1 in zip(grouped, ds):
+            assert torch.equal(torch.nan_to_num(d0, nan=7.0).view(torch.int32),
+                               torch.nan_to_num(d1, nan=7.0).view(torch.int32))
+        m, n = 100, 100
+        a_h = a.cpu().numpy().view(np.uint16)
+        b_h = b.cpu().numpy().view(np.uint16)
+        c_h = c.cpu().numpy()
+        want = O.gemm(m, n, k, a_h, k, b_h, full, c_h, full, 1.25, 0.5, ldd=full)
+        got = grouped[3].cpu().numpy()
+        for r in range(m):
+            np.testing.assert_array_less(np.abs(got[r * full:r * full + n] - want[r * full:r * full + n]),
+                                         tolerance(k, 1.0, 1.0, 1.0, 1.25, 0.5) + 1e-12)
+
+
 def test_wall_clock_trace(torch):
     spec = make_spec("plumbing16")
     dw = DeviceWorkload(spec)

@@ -161,6 +161,7 @@ SIGNATURES = {
     "ggk_device_info_get": (_i, [_P(GGKDeviceInfo)]),
     "ggk_work_shape_get": (_i, [_i, _i, _P(GGKWorkShape)]),
     "ggk_needs_addr64": (_i, [_i, _i, _P(GGDeviceProblemDesc)]),
+    "ggk_work_halves_supported": (_i, [_i, _i]),
     "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
     "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp,
                                        _vp]),

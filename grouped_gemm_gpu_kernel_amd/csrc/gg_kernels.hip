@@ -273,10 +273,13 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
     };
 
     int prob, local;
+    int half = 0;  // 0: the whole work tile; 1, 2: its first or second half of rows
     if (args.work_table != nullptr) {
       // One scalar load instead of the search's chain of dependent ones.
       prob = ((const_int_ptr)args.work_table)[2 * t];
-      local = ((const_int_ptr)args.work_table)[2 * t + 1];
+      const int word = ((const_int_ptr)args.work_table)[2 * t + 1];
+      local = word & GGK_WORK_LOCAL_MASK;
+      half = S::CLASSES ? (word >> GGK_WORK_HALF_SHIFT) & 3 : 0;
     } else {
       const int pos = find_problem(args.work_offsets, args.count, t);
       prob = args.order != nullptr ? ((const_int_ptr)args.order)[pos] : pos;
@@ -296,15 +299,26 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
         if (tid < S::TM * S::TN) {
           const int tm = wm * S::TM + tid / S::TN;
           const int tn = wn * S::TN + tid % S::TN;
-          if (tm < p.tiles_m && tn < p.tiles_n) {
+          const bool in_half = half == 0 || tid / S::TN == half - 1;
+          if (in_half && tm < p.tiles_m && tn < p.tiles_n) {
             const int ref = base + tm * p.tiles_n + tn;
             args.tile_map[3 * ref + 0] = prob;
             args.tile_map[3 * ref + 1] = tm;
             args.tile_map[3 * ref + 2] = tn;
           }
         }
-      } else {
+      } else if (half == 0) {
         run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
+      } else {
+        // One half of the rows (a whole row of macro-tiles), computed as a
+        // problem that ends with that half: its tile has at most BM / 2 rows
+        // and runs in a half-height edge class, and each of its D elements is
+        // computed as in the whole tile.
+        gg_device_problem_desc q = p;
+        const int m0 = wm * G::BM + (half - 1) * (G::BM / 2);
+        const int end = m0 + G::BM / 2;
+        q.m = end < p.m ? end : p.m;
+        run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request);
       }
     }
     if (!asked) request();
@@ -432,7 +446,7 @@ struct KernelEntry {
    {gg_grouped_kernel<V, P, true, false>, gg_grouped_kernel<V, P, true, true>},                     \
    {gg_single_kernel<V, P, false>, gg_single_kernel<V, P, true>}, KernelEntry<V, P>::threads,        \
    KernelEntry<V, P>::tm, KernelEntry<V, P>::tn, KernelEntry<V, P>::bm, KernelEntry<V, P>::bn,      \
-   KernelEntry<V, P>::bk}
+   KernelEntry<V, P>::bk, KernelShape<V, P>::CLASSES}
 #define GG_ROW(V) {GG_ENTRY(V, 0), GG_ENTRY(V, 1)}
 
 struct KernelSet {
@@ -445,6 +459,7 @@ struct KernelSet {
   int bm;  // work-tile rows
   int bn;  // work-tile columns
   int bk;  // stage depth
+  bool halves;  // reads half-work-tile table entries
 };
 
 static const KernelSet kKernels[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {
@@ -618,6 +633,11 @@ hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out) {
   out->rows = k.bm;
   out->stage_k = k.bk;
   return hipSuccess;
+}
+
+int ggk_work_halves_supported(int variant, int path) {
+  if (!valid_kernel(variant, path)) return -1;
+  return kKernels[variant][path].halves ? 1 : 0;
 }
 
 int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* problem) {

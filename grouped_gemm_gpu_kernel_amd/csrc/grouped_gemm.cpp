@@ -482,7 +482,7 @@ struct GroupedGemmExecutor::Impl {
   DeviceProblemDesc* d_problems = nullptr;
   // [problem_count + 1] reference tile offsets, then [problem_count + 1]
   // work-tile offsets in scheduling order, then [problem_count] the
-  // scheduling order, then (if work_table) [2 * total_work] the work table.
+  // scheduling order, then (if work_table) [2 * launch_total] the work table.
   int* d_ints = nullptr;
   int* d_state = nullptr;
 
@@ -498,6 +498,11 @@ struct GroupedGemmExecutor::Impl {
   int addressing = GGK_ADDR_32;
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> chunk_bounds{};
   bool work_table = false;
+  // What a launch claims: work-table entries (a work tile split into its two
+  // halves counts twice) and the chunk bounds over them; without a table,
+  // total_work and chunk_bounds.
+  int launch_total = 0;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds{};
 
   const int* d_work_table() const {
     return work_table ? d_ints + 3 * static_cast<size_t>(problem_count) + 2 : nullptr;
@@ -514,6 +519,8 @@ struct GroupedGemmExecutor::Impl {
     addressing = GGK_ADDR_32;
     chunk_bounds = {};
     work_table = false;
+    launch_total = 0;
+    launch_bounds = {};
   }
 };
 
@@ -522,6 +529,32 @@ namespace {
 // Work tables up to this many work tiles (8 bytes each) are uploaded; larger
 // sets are searched.
 constexpr int kWorkTableMax = 1 << 22;
+
+// Work tiles among the last of each chunk that the work table lists as two
+// halves (rows), for kernels that read such entries, in sets of at most
+// kTailHalvesMaxPerSlot work tiles per workgroup slot.  The workgroups of a
+// chunk run dry one by one, each after its last tile; the tiles still running
+// then decide when the launch ends, so halving the last ones (the shortest
+// of the chunk already) cuts the time the others wait.  A half costs more
+// than half a tile (it stages all of the tile's B), so sets whose launch is
+// long against one tile keep whole tiles: there the tail is a small share.
+#ifndef GG_TAIL_HALVES
+#define GG_TAIL_HALVES 64
+#endif
+constexpr int kTailHalves = GG_TAIL_HALVES;
+constexpr int kTailHalvesMaxPerSlot = 12;
+
+// Row of work tiles of work tile `local` in a problem with wtm x wtn of them,
+// in the grouped kernel's order (groups of 4 rows, column by column within a
+// group; gg_kernels.hip, work_tile_position).
+int work_tile_row(int local, int wtm, int wtn) {
+  constexpr int kGroupRows = 4;
+  const int group = local / (kGroupRows * wtn);
+  const int first = group * kGroupRows;
+  const int rows = std::min(kGroupRows, wtm - first);
+  const int within = local - group * kGroupRows * wtn;
+  return first + within % rows;
+}
 
 }  // namespace
 
@@ -637,13 +670,47 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   OccupancyInfo occupancy{};
   status = cached_occupancy(config, mode, &occupancy);
   if (status != hipSuccess) return status;
+  // The persistent grid is sized by the units it claims: work tiles.
+  const int grid_slots = grid_ctas_for(total_work, config, occupancy);
 
   // Device ints: the reference tile offsets (sorted order), the work-tile
   // offsets (scheduling order), the scheduling order, then the work table --
   // (problem, work tile within it) of every work-tile index, so that the
   // kernel reads it with one load instead of searching.
-  const size_t int_count = 3 * static_cast<size_t>(problem_count) + 2 +
-                           (work_table ? 2 * static_cast<size_t>(total_work) : 0);
+  // The work table in claim order.  Within the last kTailHalves entries of
+  // each chunk, a work tile with more than half its rows inside the problem
+  // is listed as its two halves, consecutively.
+  std::vector<int> table;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds = schedule.bounds;
+  if (work_table) {
+    const bool halves = kTailHalves > 0 && ggk_work_halves_supported(mode.variant, mode.path) == 1 &&
+                        total_work <= kTailHalvesMaxPerSlot * grid_slots;
+    const int bm = config.cta_m * mode.work.tiles_m;
+    table.reserve(2 * static_cast<size_t>(total_work) + 4 * GGK_SCHEDULER_CHUNKS * std::max(kTailHalves, 0));
+    int index = 0;  // work-tile index of the entry being listed
+    int chunk = 0;
+    launch_bounds[0] = 0;
+    for (const int prob : schedule.order) {
+      const DeviceProblemDesc& dp = device_problems[prob];
+      const int wtm = ceil_div(dp.tiles_m, mode.work.tiles_m);
+      const int wtn = ceil_div(dp.tiles_n, mode.work.tiles_n);
+      for (int w = 0; w < work[prob]; ++w, ++index) {
+        while (chunk < GGK_SCHEDULER_CHUNKS && index >= schedule.bounds[chunk + 1]) {
+          launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
+        }
+        const bool tail = halves && index >= schedule.bounds[chunk + 1] - kTailHalves;
+        if (tail && dp.m - work_tile_row(w, wtm, wtn) * bm > bm / 2) {
+          table.insert(table.end(), {prob, w | (1 << GGK_WORK_HALF_SHIFT), prob, w | (2 << GGK_WORK_HALF_SHIFT)});
+        } else {
+          table.insert(table.end(), {prob, w});
+        }
+      }
+    }
+    while (chunk < GGK_SCHEDULER_CHUNKS) launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
+  }
+  const int launch_total = work_table ? static_cast<int>(table.size() / 2) : total_work;
+
+  const size_t int_count = 3 * static_cast<size_t>(problem_count) + 2 + table.size();
   const size_t desc_bytes = DeviceBuffer::round256(problem_count * sizeof(DeviceProblemDesc));
   const size_t int_bytes = DeviceBuffer::round256(int_count * sizeof(int));
   const size_t state_bytes = DeviceBuffer::round256(GGK_SCHEDULER_STATE_INTS * sizeof(int));
@@ -654,14 +721,7 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   ints = std::copy(prepared.tile_offsets.begin(), prepared.tile_offsets.end(), ints);
   ints = std::copy(schedule.work_offsets.begin(), schedule.work_offsets.end(), ints);
   ints = std::copy(schedule.order.begin(), schedule.order.end(), ints);
-  if (work_table) {
-    for (const int prob : schedule.order) {
-      for (int w = 0; w < work[prob]; ++w) {
-        *ints++ = prob;
-        *ints++ = w;
-      }
-    }
-  }
+  ints = std::copy(table.begin(), table.end(), ints);
 
   status = impl_->buffer.reserve(total_bytes);
   if (status != hipSuccess) return status;
@@ -681,8 +741,9 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   impl_->addressing = addressing;
   impl_->chunk_bounds = schedule.bounds;
   impl_->work_table = work_table;
-  // The persistent grid is sized by the units it claims: work tiles.
-  impl_->grid_ctas = grid_ctas_for(total_work, config, occupancy);
+  impl_->launch_total = launch_total;
+  impl_->launch_bounds = launch_bounds;
+  impl_->grid_ctas = grid_slots;
   impl_->failed = false;
   return hipSuccess;
 }
@@ -697,8 +758,8 @@ hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   const hipError_t status =
       ggk_launch_grouped(impl_->variant, impl_->path, impl_->addressing, impl_->d_problems,
                          impl_->d_ints + impl_->problem_count + 1, impl_->d_ints + 2 * (impl_->problem_count + 1),
-                         impl_->d_work_table(), impl_->problem_count, impl_->total_work, impl_->d_state,
-                         impl_->chunk_bounds.data(), impl_->grid_ctas, stream);
+                         impl_->d_work_table(), impl_->problem_count, impl_->launch_total, impl_->d_state,
+                         impl_->launch_bounds.data(), impl_->grid_ctas, stream);
   if (status != hipSuccess) return status;
   return impl_->buffer.note_launch(stream);
 }
@@ -710,7 +771,7 @@ hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_cloc
   const hipError_t status = ggk_launch_grouped_traced(
       impl_->variant, impl_->path, impl_->addressing, impl_->d_problems, impl_->d_ints,
       impl_->d_ints + impl_->problem_count + 1, impl_->d_ints + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
-      impl_->problem_count, impl_->total_work, impl_->d_state, impl_->chunk_bounds.data(), impl_->grid_ctas, d_tile_map,
+      impl_->problem_count, impl_->launch_total, impl_->d_state, impl_->launch_bounds.data(), impl_->grid_ctas, d_tile_map,
       d_wg_clock, stream);
   if (status != hipSuccess) return status;
   return impl_->buffer.note_launch(stream);

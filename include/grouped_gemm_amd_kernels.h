@@ -78,6 +78,15 @@ enum { GGK_KERNEL_GROUPED = 0, GGK_KERNEL_SINGLE = 1 };
  * line. */
 #define GGK_SCHEDULER_COUNTER_STRIDE 32
 
+/* A work-table entry's second int: the work tile's index within its problem
+ * in the low bits (GGK_WORK_LOCAL_MASK), and in bits GGK_WORK_HALF_SHIFT and
+ * up 0 for the whole work tile or 1 / 2 for its first / second half of rows
+ * (one row of macro-tiles each; only for kernels whose work tile is two
+ * macro-tiles tall and that have half-height edge classes:
+ * ggk_work_halves_supported). */
+#define GGK_WORK_HALF_SHIFT 28
+#define GGK_WORK_LOCAL_MASK ((1 << GGK_WORK_HALF_SHIFT) - 1)
+
 /* Ints of scheduler state one grouped launch needs: a claim counter per chunk
  * and a retire counter, GGK_SCHEDULER_COUNTER_STRIDE apart.  Must be zero
  * before the first launch; every launch leaves it zero again. */
@@ -171,6 +180,11 @@ typedef struct ggk_work_shape {
 } ggk_work_shape;
 hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out);
 
+/* 1 when the grouped kernel of (variant, path) reads work-table entries for
+ * half work tiles (GGK_WORK_HALF_SHIFT), 0 when it does not, -1 for a bad
+ * argument.  No reference counterpart. */
+int ggk_work_halves_supported(int variant, int path);
+
 /* Addressing form of a grouped launch.  GGK_ADDR_32: A and B are addressed
  * and C/D with 32-bit offsets from per-tile origins, which needs, for every
  * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda + k + 8 * stage_k <
@@ -197,8 +211,10 @@ int ggk_needs_addr64(int variant, int path, const gg_device_problem_desc* proble
  * for equal counts) splits the work-tile indices into the per-XCD chunks.
  * d_work_table[2 * total_work] (device memory, or NULL) holds for each
  * work-tile index the problem (in sorted order) and the work tile's index
- * within that problem (numbered as described at ggk_work_shape), which the kernel then reads instead of
- * searching d_work_offsets for them.  grid workgroups claim work tiles until
+ * within that problem (numbered as described at ggk_work_shape, encoded as
+ * at GGK_WORK_HALF_SHIFT), which the kernel then reads instead of
+ * searching d_work_offsets for them; a table may list both halves of a work
+ * tile instead of the whole, and then counts them as two work-tile indices.  grid workgroups claim work tiles until
  * total_work are done. */
 hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
                               const int* d_work_offsets, const int* d_order, const int* d_work_table,

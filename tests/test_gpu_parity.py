@@ -159,6 +159,9 @@ def _mapping_sets():
     sets["small256"] = list(zip(m, n, k))
     spec = make_spec("longtail4096")
     sets["longtail4096"] = list(zip(spec.m, spec.n, spec.k))
+    # short enough a launch for the work table to list the last tiles of each chunk as halves
+    spec = make_spec("mixed512")
+    sets["mixed512"] = list(zip(spec.m, spec.n, spec.k))
     cnt = 5000
     mm = rng.integers(0, 300, cnt)
     mm[rng.random(cnt) < 0.3] = 0  # many zero-tile problems

@@ -21,8 +21,10 @@ All work runs in the HIP library (lib/libgrouped_gemm_amd.so); there is no CPU f
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence, Union
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -114,6 +116,83 @@ def _problems(a, b, c, d, alpha, beta):
     return problems
 
 
+# gg_problem_desc (include/grouped_gemm_amd.h) as a numpy record: one array of them is passed to the
+# C ABI as is.
+_DESC_DTYPE = np.dtype([("m", "<i4"), ("n", "<i4"), ("k", "<i4"), ("_pad", "<i4"), ("a", "<u8"), ("b", "<u8"),
+                        ("c", "<u8"), ("d", "<u8"), ("lda", "<i4"), ("ldb", "<i4"), ("ldc", "<i4"),
+                        ("ldd", "<i4"), ("alpha", "<f4"), ("beta", "<f4")])
+assert _DESC_DTYPE.itemsize == ctypes.sizeof(_lib.GGProblemDesc)
+
+
+def _ld(shape, stride) -> int:
+    """_row_stride from a shape and stride already read."""
+    rows, cols = shape
+    if rows <= 1 or rows * cols == 0:
+        return max(1, cols)
+    return stride[0]
+
+
+def _problem_table(a, b, c, d, alpha, beta) -> np.ndarray:
+    """The problems of tensor lists as gg_problem_desc records, with the checks of _problems: each
+    tensor's metadata is read once, in bulk, and any failed check is reported by _problems' own
+    per-tensor messages."""
+    count = len(a)
+    if len(b) != count or len(d) != count or (c is not None and len(c) != count):
+        raise ValueError("a, b, c and d must hold one tensor per problem")
+    table = np.zeros(count, _DESC_DTYPE)
+    if count == 0:
+        return table
+    device = a[0].device
+    if device.type != "cuda":
+        raise ValueError(f"tensors must be on a GPU, got {device}")
+    cs = list(c) if c is not None else [None] * count
+    f16, f32 = torch.float16, torch.float32
+    try:
+        sa = [t.shape for t in a]
+        sb = [t.shape for t in b]
+        sd = [t.shape for t in d]
+        ok = (all(t.dtype is f16 and t.device == device for t in a) and
+              all(t.dtype is f16 and t.device == device for t in b) and
+              all(t.dtype is f32 and t.device == device for t in d) and
+              all(t is None or (t.dtype is f32 and t.device == device) for t in cs) and
+              all(len(x) == 2 and len(y) == 2 and x[1] == y[0] for x, y in zip(sa, sb)) and
+              all(z == (x[0], y[1]) for x, y, z in zip(sa, sb, sd)) and
+              all(t is None or t.shape == z for t, z in zip(cs, sd)))
+        if ok:
+            ta = [t.stride() for t in a]
+            tb = [t.stride() for t in b]
+            td = [t.stride() for t in d]
+            tc = [t.stride() if t is not None else None for t in cs]
+            # rows contiguous and not overlapping (see _check_matrix)
+            for shapes, strides in ((sa, ta), (sb, tb), (sd, td)):
+                ok = ok and all((x[1] <= 1 or s[1] == 1 or x[0] * x[1] == 0) and
+                                (x[0] <= 1 or s[0] >= max(1, x[1]) or x[0] * x[1] == 0)
+                                for x, s in zip(shapes, strides))
+            ok = ok and all(t is None or ((z[1] <= 1 or s[1] == 1 or z[0] * z[1] == 0) and
+                                          (z[0] <= 1 or s[0] >= max(1, z[1]) or z[0] * z[1] == 0))
+                            for t, s, z in zip(cs, tc, sd))
+    except (AttributeError, TypeError):
+        ok = False
+    if not ok:
+        _problems(a, b, c, d, alpha, beta)  # raises with the failed check's message
+        raise ValueError("tensor lists do not describe grouped GEMM problems")
+    dummy = _placeholder(device)
+    table["m"] = [x[0] for x in sa]
+    table["k"] = [x[1] for x in sa]
+    table["n"] = [x[1] for x in sb]
+    table["a"] = [t.data_ptr() or dummy for t in a]
+    table["b"] = [t.data_ptr() or dummy for t in b]
+    table["d"] = [t.data_ptr() or dummy for t in d]
+    table["c"] = [(t.data_ptr() or dummy) if t is not None else 0 for t in cs]
+    table["lda"] = [_ld(x, s) for x, s in zip(sa, ta)]
+    table["ldb"] = [_ld(x, s) for x, s in zip(sb, tb)]
+    table["ldd"] = [_ld(x, s) for x, s in zip(sd, td)]
+    table["ldc"] = [_ld(z, s) if t is not None else max(1, z[1]) for t, s, z in zip(cs, tc, sd)]
+    table["alpha"] = _per_problem(alpha, count, "alpha")
+    table["beta"] = _per_problem(beta, count, "beta")
+    return table
+
+
 class GroupedGemmPlan:
     """A prepared grouped GEMM over fixed tensors: prepare_problem_set + executor build once,
     run() per use.  Runs are stream-ordered and must not overlap each other (one scheduler state
@@ -161,11 +240,18 @@ def run_grouped_gemm(a: Sequence[torch.Tensor], b: Sequence[torch.Tensor],
             raise ValueError("a and b must hold one tensor per problem")
         out = [torch.empty((ai.shape[0], bi.shape[1] if bi.dim() == 2 else 0), dtype=torch.float32,
                            device=ai.device) for ai, bi in zip(a, b)]
-    plan = GroupedGemmPlan(a, b, c, out, alpha, beta, sort_mode=sort_mode, config=config)
-    try:
-        plan.run()
-    finally:
-        plan.close()  # synchronises the device, then releases the plan's descriptor buffers
+    # One C call (prepare, build, launch, wait, release) on a table read from the tensors in bulk.
+    table = _problem_table(a, b, c, out, alpha, beta)
+    if len(table) == 0:
+        return list(out)
+    config = config if config is not None else KernelConfig.named("128x64x32")
+    device = a[0].device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        status = _lib.lib().gg_run_grouped_gemm_once(
+            table.ctypes.data_as(ctypes.POINTER(_lib.GGProblemDesc)), len(table), int(sort_mode),
+            ctypes.byref(config.to_c()), stream or None)
+    _lib.check(status, "run_grouped_gemm_once")
     return list(out)
 
 

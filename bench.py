@@ -357,6 +357,7 @@ MFMA_CYCLES = 32        # v_mfma_f32_32x32x16_f16: cycles a SIMD is busy per ins
 MFMA_MACS = 32 * 32 * 16
 SIMDS_PER_CU = 4
 XCDS = 8
+CUS = 256
 
 
 def _derived(metrics, workload) -> list:
@@ -367,7 +368,14 @@ def _derived(metrics, workload) -> list:
                        workload's useful MFMAs (sum m n k / 16384): padding of partial tiles;
       l2_hit           TCC_HIT / (TCC_HIT + TCC_MISS);
       lds_bank_conflict  SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (cycles);
-      clock_ghz        GRBM_GUI_ACTIVE / 8 XCDs / the dispatch's duration (when traced)."""
+      clock_ghz        GRBM_GUI_ACTIVE / 8 XCDs / the dispatch's duration (when traced);
+    and, per CU (GRBM_GUI_ACTIVE / 8 cycles of the dispatch, 256 CUs):
+      ta_busy          TA_TA_BUSY / (256 x cycles): share of cycles the address unit is busy;
+      l1_l2_latency    TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ: cycles per 128-byte L1 -> L2
+                       read request;
+      l1_l2_in_flight  TCP_TCC_READ_REQ_LATENCY / (256 x cycles): mean read requests in flight per
+                       CU (Little's law);
+      l1_l2_bytes_per_cycle  128 x TCP_TCC_READ_REQ / (256 x cycles)."""
     mean = {k: sum(v) / len(v) for k, v in metrics.items()}
     out = []
     if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
@@ -385,6 +393,14 @@ def _derived(metrics, workload) -> list:
         out.append(f"lds_bank_conflict: {mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_LDS_IDX_ACTIVE']:.4f}")
     if "GRBM_GUI_ACTIVE" in mean and mean.get("duration_us"):
         out.append(f"clock_ghz: {mean['GRBM_GUI_ACTIVE'] / XCDS / (mean['duration_us'] * 1e3):.3f}")
+    cu_cycles = CUS * mean["GRBM_GUI_ACTIVE"] / XCDS if mean.get("GRBM_GUI_ACTIVE") else None
+    if cu_cycles and "TA_TA_BUSY" in mean:
+        out.append(f"ta_busy: {mean['TA_TA_BUSY'] / cu_cycles:.4f}")
+    if mean.get("TCP_TCC_READ_REQ") and "TCP_TCC_READ_REQ_LATENCY" in mean:
+        out.append(f"l1_l2_latency: {mean['TCP_TCC_READ_REQ_LATENCY'] / mean['TCP_TCC_READ_REQ']:.1f}")
+        if cu_cycles:
+            out.append(f"l1_l2_in_flight: {mean['TCP_TCC_READ_REQ_LATENCY'] / cu_cycles:.1f}")
+            out.append(f"l1_l2_bytes_per_cycle: {128 * mean['TCP_TCC_READ_REQ'] / cu_cycles:.2f}")
     return out
 
 
@@ -399,6 +415,17 @@ def profile_summary(dirs, kernel_filter: str, names=(), last: int = 0, workload=
         for (kname, seg), metrics in _segments(_dispatches(d), kernel_filter, names, last).items():
             for key, v in sorted(metrics.items()):
                 print(f"{kname} [{seg}] {key}: {_stats(v)}")
+            for line in _derived(metrics, workload):
+                print(f"{kname} [{seg}] {line}")
+    if len(dirs) > 1:
+        # Counters collected in separate runs of the same command: ratios across them.
+        merged = {}
+        for d in dirs:
+            for key, metrics in _segments(_dispatches(Path(d)), kernel_filter, names, last).items():
+                for name, v in metrics.items():
+                    merged.setdefault(key, {}).setdefault(name, []).extend(v)
+        print("== all folders")
+        for (kname, seg), metrics in merged.items():
             for line in _derived(metrics, workload):
                 print(f"{kname} [{seg}] {line}")
     return 0

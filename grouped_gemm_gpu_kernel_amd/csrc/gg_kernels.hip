@@ -272,6 +272,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       return true;
     };
 
+    static_assert(!S::CLASSES || S::TM == 2, "a half of the rows is one row of macro-tiles");
     int prob, local;
     int half = 0;  // 0: the whole work tile; 1, 2: its first or second half of rows
     if (args.work_table != nullptr) {

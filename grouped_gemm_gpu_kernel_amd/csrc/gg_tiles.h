@@ -283,6 +283,105 @@ struct MfmaTile {
   // vectors of the next chunk (two, for blocks of three or more chunks) are
   // requested before the current one is written, so their latencies overlap.  Stores go through the same kind of resource; columns that cross
   // N go element by element.
+  // D = alpha * acc + beta * C for a wave block two 32-column blocks wide (FN == 2), written so
+  // that one 16-byte access instruction covers 4 rows x 64 columns (256 contiguous bytes of each
+  // row) instead of 8 rows x 32 columns.  After the quad transpose, lane (h, c) holds row
+  // 8g + 4h + (c & 3) of both column blocks; one v_permlane32_swap per value then gives every
+  // lane rows 8g + (c & 3) and 8g + 4 + (c & 3), lanes 0..31 of column block 0 and lanes 32..63
+  // of block 1.  Rows of tightly packed matrices (ldc = ldd = N) seldom start on a 128-byte line,
+  // and 256 contiguous bytes of such a row span 3 lines where two separate 128-byte pieces span
+  // 4: C reads and D writes make a quarter fewer L1 -> L2 requests.  Loading C, multiplying and
+  // storing follow store_tile (chunks of EPI_ROWS accumulator rows, the next chunks' C requested
+  // ahead).
+  __device__ __forceinline__ static void store_pairs(const gg_device_problem_desc& p, int r0, int c0, int lane,
+                                                     const floatx16_t (&acc)[FM][FN], bool use_c) {
+    static_assert(FN == 2, "two 32-column blocks");
+    const int q = lane & 3;
+    const int col = 32 * (lane >> 5) + ((lane & 31) & ~3);  // first of the lane's 4 columns in the block
+    const int ncol = p.n - (c0 + col);                        // how many of them lie inside the matrix
+    const __amdgpu_buffer_rsrc_t drs =
+        buffer_rsrc(p.d + ((int64_t)r0 * p.ldd + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldd + (p.n - c0)));
+    constexpr int CHUNKS = FM / EPI_ROWS;
+    constexpr int AHEAD = CHUNKS >= 3 ? GG_EPI_AHEAD : 1;
+    // C vectors of a chunk: [accumulator row][row group g][rows 8g + q, 8g + 4 + q].
+    floatx4_t cv[AHEAD + 1][EPI_ROWS][4][2];
+    auto load_c = [&](int chunk, floatx4_t (&dst)[EPI_ROWS][4][2]) {
+      if (use_c) {
+        const __amdgpu_buffer_rsrc_t crs =
+            buffer_rsrc(p.c + ((int64_t)r0 * p.ldc + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldc + (p.n - c0)));
+#pragma unroll
+        for (int i = 0; i < EPI_ROWS; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              const int row = (chunk * EPI_ROWS + i) * 32 + 8 * g + 4 * hf + q;
+              // Vectors wholly past N would read the next row's head: an offset past the resource.
+              const uint32_t off =
+                  ncol > 0 ? 4u * ((uint32_t)row * (uint32_t)p.ldc + col) : DmaLoader<G>::kOutOfRange;
+              dst[i][g][hf] =
+                  __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(crs, (int)off, 0, 0));
+            }
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPI_ROWS; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) dst[i][g][hf] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    };
+#pragma unroll
+    for (int c = 0; c < AHEAD; ++c) {
+      if (c < CHUNKS) load_c(c, cv[c]);
+    }
+#pragma unroll
+    for (int chunk = 0; chunk < CHUNKS; ++chunk) {
+      if (chunk + AHEAD < CHUNKS) load_c(chunk + AHEAD, cv[(chunk + AHEAD) % (AHEAD + 1)]);
+#pragma unroll
+      for (int i = 0; i < EPI_ROWS; ++i) {
+        const int fm = chunk * EPI_ROWS + i;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v0[4] = {acc[fm][0][4 * g + 0], acc[fm][0][4 * g + 1], acc[fm][0][4 * g + 2], acc[fm][0][4 * g + 3]};
+          float v1[4] = {acc[fm][1][4 * g + 0], acc[fm][1][4 * g + 1], acc[fm][1][4 * g + 2], acc[fm][1][4 * g + 3]};
+          quad_transpose(v0, q);
+          quad_transpose(v1, q);
+          float vh[2][4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0[e]), __float_as_uint(v1[e]), false,
+                                                            false);
+            vh[0][e] = __uint_as_float(r[0]);
+            vh[1][e] = __uint_as_float(r[1]);
+          }
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int row = fm * 32 + 8 * g + 4 * hf + q;
+            floatx4_t out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              out[e] = epilogue_value(vh[hf][e], cv[chunk % (AHEAD + 1)][i][g][hf][e], p.alpha, p.beta);
+            }
+            if (r0 + row >= p.m || ncol <= 0) continue;
+            const uint32_t off = 4u * ((uint32_t)row * (uint32_t)p.ldd + col);
+            if (ncol >= 4) {
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(__attribute__((ext_vector_type(4))) int, out), drs, (int)off, 0, 0);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 3; ++e) {
+                if (e < ncol) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(out[e]), drs, (int)(off + 4 * e), 0, 0);
+              }
+            }
+          }
+        }
+      }
+      // Keep each chunk's loads and stores in place (see store_tile).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
   template <bool WIDE>
   __device__ __forceinline__ static void store_tile(const gg_device_problem_desc& p, int r0, int c0, int lane,
                                                     const floatx16_t (&acc)[FM][FN]) {
@@ -290,7 +389,9 @@ struct MfmaTile {
     const int q = lane & 3;
     const int lrow = 4 * (lane >> 5) + q;  // row within an 8-row group
     const int lcol = (lane & 31) & ~3;     // first column of the lane's vector
-    if constexpr (!WIDE) {
+    if constexpr (!WIDE && FN == 2) {
+      store_pairs(p, r0, c0, lane, acc, use_c);
+    } else if constexpr (!WIDE) {
       const __amdgpu_buffer_rsrc_t drs =
           buffer_rsrc(p.d + ((int64_t)r0 * p.ldd + c0), 4 * ((int64_t)(p.m - 1 - r0) * p.ldd + (p.n - c0)));
       // C vectors of EPI_ROWS 32-row groups per chunk; the C of the next

@@ -489,6 +489,8 @@ int main(int argc, char** argv) {
         singles.error = v.error;
       } else {
         singles.solution = "hipblasLtMatmul per problem (heuristic first choice)";
+        if (!v.mm.empty())
+          singles.solution += "; first problem: " + hipblaslt_ext::getSolutionNameFromAlgo(v.handle, v.mm[0].algo);
         HIP_OK(ggk_fill_f32(pools.d_vendor, std::max<int64_t>(pools.d_n, 1), NAN, nullptr));
         if (per_problem_run(&v) != 0) singles.error = "hipblasLtMatmul failed";
         HIP_OK(hipDeviceSynchronize());

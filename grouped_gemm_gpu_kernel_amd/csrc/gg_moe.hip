@@ -124,6 +124,9 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   __shared__ int s_order[kMaxExperts];       // sorted position at each scheduling position
   __shared__ int s_work[kMaxExperts];        // work tiles of sorted position i
   __shared__ int s_chunk_work[kChunks];
+  __shared__ long long s_load[kChunks];  // chunk loads of the whole placement
+  __shared__ int s_cut[kChunks + 1];  // chunk bounds inside the run of oversized positions
+  __shared__ int s_run[3];            // oversized positions cut across chunks (0: none), first LPT chunk, run's work tiles
   __shared__ int s_status;
 
   const ggk_moe_layout& L = args.layout;
@@ -229,10 +232,17 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   if (pos == 0) args.offsets[experts] = total_tiles;
 
   // The schedule, as the host build plans it (plan_schedule in
-  // grouped_gemm.cpp): longest processing time first at two levels.  Sorted
-  // positions go whole to the chunk with the least estimated time so far,
-  // longest first (ties: lower position first); within a chunk they run
-  // longest work tile first (ties: lower position first).
+  // grouped_gemm.cpp): longest processing time first at two levels, after
+  // spreading oversized positions.  One share is the total estimated time over
+  // the chunks, rounded up.  Sorted positions above one share are cut across
+  // chunks when placing every position whole (longest first, ties: lower
+  // position first, each onto the first least-loaded chunk) would leave more
+  // than a quarter of the total to stealing: they run first, back to back,
+  // longest first, and chunk boundary c falls at the work tile nearest to where
+  // the run's time reaches c shares.  The other positions go whole to the first
+  // least-loaded chunk from the one holding the run's end on (which starts
+  // with the remainder), longest first; within a chunk they run longest work
+  // tile first (ties: lower position first), after the run.
   long long total = 0;  // estimated time, clamped (problem_time_units)
   double key = 0.0;     // estimated time per work tile
   if (pos < experts) {
@@ -247,7 +257,10 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     s_key[pos] = key;
     s_work[pos] = work;
   }
-  __syncthreads();
+  // At most GGK_MOE_MAX_EXPERTS (2^10) totals of at most 2^52: the sum is exact.
+  long long sum_all;
+  (void)block_exclusive_scan<long long>(total, s_waves_ll, &sum_all);
+  const long long share = sum_all / kChunks + (sum_all % kChunks != 0 ? 1 : 0);
   if (pos < experts) {
     int rank = 0;
 #pragma unroll 8
@@ -259,17 +272,16 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     s_order[rank] = pos;
   }
   __syncthreads();
-  if (tid < kWave) {
-    // Greedy assignment by wave 0, one position at a time onto the first
-    // least-loaded chunk.  Lane c < kChunks holds chunk c's load (an exact
-    // integer), the other lanes a load no chunk reaches; the least (load,
-    // lane) pair reaches lane 0 in three row shifts, so ties go to the lower
-    // chunk as in a scan.  The estimated times come from LDS 64 at a time, one
-    // per lane; each step takes its own from its lane and leaves its choice
-    // in that lane.
-    const int lane = tid;
-    unsigned long long load = lane < kChunks ? 0ull : ~0ull;
-    for (int r0 = 0; r0 < experts; r0 += kWave) {
+  // Greedy assignment by wave 0, one position at a time onto the first
+  // least-loaded chunk.  Lane c < kChunks holds chunk c's load (an exact
+  // integer), the other lanes a load no chunk reaches; the least (load, lane)
+  // pair reaches lane 0 in three row shifts, so ties go to the lower chunk as
+  // in a scan.  The estimated times come from LDS 64 at a time, one per lane;
+  // each step takes its own from its lane and leaves its choice in that lane.
+  // Returns each lane's final load.
+  const int lane = tid & (kWave - 1);
+  auto greedy = [&](int from, unsigned long long load) {
+    for (int r0 = from; r0 < experts; r0 += kWave) {
       const int r = r0 + lane;
       const unsigned long long mine = r < experts ? (unsigned long long)s_by_total[r] : 0ull;
       const int mine_lo = (int)(uint32_t)mine;
@@ -277,9 +289,8 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
       const int steps = min(kWave, experts - r0);
       int chosen = 0;  // lane j: the chunk of by-total rank r0 + j
       for (int j = 0; j < steps; ++j) {
-        const unsigned long long t =
-            ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane(mine_hi, j) << 32) |
-            (uint32_t)__builtin_amdgcn_readlane(mine_lo, j);
+        const unsigned long long t = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane(mine_hi, j) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane(mine_lo, j);
         unsigned long long v = load;
         int idx = lane;
         least_from<4>(v, idx);
@@ -291,6 +302,54 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
       }
       if (r < experts) s_chunk[s_order[r]] = chosen;
     }
+    return load;
+  };
+  // Every position placed whole.
+  if (tid < kWave) {
+    const unsigned long long load = greedy(0, lane < kChunks ? 0ull : ~0ull);
+    if (lane < kChunks) s_load[lane] = (long long)load;
+  }
+  __syncthreads();
+  if (tid == 0) {
+#pragma clang fp contract(off)
+    int oversized = 0;  // they lead the by-total order
+    while (oversized < experts && oversized < kChunks && s_by_total[oversized] > share) ++oversized;
+    if (oversized > 0) {
+      double stolen = 0.0;  // the chunks' shortfall below one share, in chunk order
+      for (int c = 0; c < kChunks; ++c) stolen += s_load[c] < share ? (double)(share - s_load[c]) : 0.0;
+      if (stolen * 4.0 <= (double)sum_all) oversized = 0;
+    }
+    int first = 0, run_work = 0;
+    long long run_time = 0;
+    if (oversized > 0) {
+      int c = 1;
+      for (int r = 0; r < oversized; ++r) {
+        const int i = s_order[r];
+        const long long t = s_by_total[r];
+        const int w = s_work[i];
+        for (; c < kChunks && c * share < run_time + t; ++c) {
+          const double x = (double)(c * share - run_time) / (double)t * w;
+          const int j = (int)floor(x + 0.5);
+          s_cut[c] = run_work + (j < 0 ? 0 : (j > w ? w : j));
+        }
+        s_chunk[i] = r - kChunks;  // ahead of every chunk, in run order
+        run_time += t;
+        run_work += w;
+      }
+      first = c - 1;
+      s_cut[0] = 0;
+    }
+    s_run[0] = oversized;
+    s_run[1] = first;
+    s_run[2] = run_work;
+    s_load[0] = run_time - first * share;  // the first open chunk's starting load
+  }
+  __syncthreads();
+  // The other positions, onto chunks from the one holding the run's end.
+  if (tid < kWave && s_run[0] > 0) {
+    const int first = s_run[1];
+    const unsigned long long start = (unsigned long long)s_load[0];
+    (void)greedy(s_run[0], lane < first || lane >= kChunks ? ~0ull : (lane == first ? start : 0ull));
   }
   __syncthreads();
   int chunk = 0;
@@ -311,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
                                                                                                              : 0;
       }
     }
-    atomicAdd(&s_chunk_work[chunk], work);
+    if (chunk >= 0) atomicAdd(&s_chunk_work[chunk], work);
     s_order[before] = pos;  // its by-total contents were last read by the greedy pass
   }
   __syncthreads();
@@ -327,10 +386,17 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     args.offsets[2 * experts + 1] = total_work;
     args.header[0] = total_tiles;
     args.header[1] = total_work;
-    int bound = 0;
+    // Chunks up to the one holding the run's end start where the run was cut.
+    const int split = s_run[0] > 0;
+    const int first = s_run[1];
+    int bound = split ? s_run[2] : 0;
     for (int c = 0; c < kChunks; ++c) {
-      args.header[2 + c] = bound;
-      bound += s_chunk_work[c];
+      if (split && c <= first) {
+        args.header[2 + c] = s_cut[c];
+      } else {
+        args.header[2 + c] = bound;
+      }
+      if (c >= first) bound += s_chunk_work[c];
     }
     args.header[2 + kChunks] = bound;
     for (int h = 3 + kChunks; h < GGK_MOE_HEADER_INTS; ++h) args.header[h] = 0;

@@ -8,9 +8,11 @@
 
 #include <algorithm>
 #include <array>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <numeric>
 #include <tuple>
@@ -214,6 +216,7 @@ hipError_t cached_occupancy(const KernelConfig& config, const RuntimeMode& mode,
 struct Schedule {
   std::vector<int> order;         // problem (sorted index) at each position
   std::vector<int> work_offsets;  // prefix sums of the work-tile counts in that order
+  std::vector<double> tile_time;  // estimated time of one work tile of the problem at each position
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> bounds{};
 };
 
@@ -246,11 +249,22 @@ double problem_work_time(int m, int n, int k, int tm, int tn, int bk, bool reads
 // beyond that.
 int64_t problem_time_units(double t) { return t < 4503599627370496.0 ? static_cast<int64_t>(t) : (int64_t{1} << 52); }
 
-// Longest processing time first at two levels.  Problems go whole to the XCD
-// chunk with the least estimated work so far, largest problems first (a
-// problem's tiles share A and B panels, which that XCD's L2 then serves);
-// within a chunk the tiles with the longest estimated time come first, so
-// the last tiles any workgroup starts are short ones.  Every order yields the
+// Longest processing time first at two levels, after spreading oversized
+// problems.  A problem whose estimated time exceeds one chunk's share (the
+// total over the chunks, rounded up) would overload whichever chunk took it
+// whole: the other XCDs would then take its tiles one claim at a time,
+// interleaved, and each XCD's L2 would hold scattered panels of it.  Such
+// problems run first instead, back to back, largest first, and the chunk
+// boundaries cut that run into consecutive pieces of one share each (at the
+// work tile nearest to where the run's estimated time reaches c shares), so
+// that each XCD multiplies a contiguous block of their tiles.  The other
+// problems go whole to the chunk with the least estimated work so far (the
+// chunk that holds the end of the run starts with its remainder), largest
+// first (a problem's tiles share A and B panels, which that XCD's L2 then
+// serves); within a chunk the tiles with the longest estimated time come
+// first, after the run's remainder (which stays contiguous with its earlier
+// pieces), so the last tiles any workgroup starts are short ones.  Without
+// oversized problems this is the two-level LPT alone.  Every order yields the
 // same D: each work tile is computed the same way wherever it runs.
 Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std::vector<int>& work, int bm, int bn,
                        int bk) {
@@ -258,6 +272,7 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
   const int count = static_cast<int>(problems.size());
   std::vector<double> tile_time(count);
   std::vector<int64_t> total(count);
+  int64_t sum = 0;  // saturating
   for (int i = 0; i < count; ++i) {
     const DeviceProblemDesc& p = problems[i];
     const bool reads_c = p.c != nullptr && p.beta != 0.0f;
@@ -266,34 +281,80 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
     const double t = work[i] > 0 ? problem_work_time(p.m, p.n, p.k, tm, tn, bk, reads_c) : 0.0;
     total[i] = problem_time_units(t);
     tile_time[i] = work[i] > 0 ? t / work[i] : 0.0;
+    sum = sum > INT64_MAX - total[i] ? INT64_MAX : sum + total[i];
   }
+  const int64_t share = sum / kChunks + (sum % kChunks != 0 ? 1 : 0);
   std::vector<int> by_total(count);
   for (int i = 0; i < count; ++i) by_total[i] = i;
   std::stable_sort(by_total.begin(), by_total.end(), [&](int x, int y) { return total[x] > total[y]; });
+  int oversized = 0;  // they lead by_total
+  while (oversized < count && total[by_total[oversized]] > share) ++oversized;
+  if (oversized > 0) {
+    // Placed whole, the oversized problems leave other chunks short of a
+    // share, and those XCDs take the difference from the overloaded chunks by
+    // stealing.  Stealing a little is cheap (and balances at run time what
+    // the estimate misjudged); the run is cut only when whole placement would
+    // leave more than a quarter of the work to it.
+    std::array<int64_t, kChunks> whole{};
+    for (const int i : by_total) {
+      int c = 0;
+      for (int d = 1; d < kChunks; ++d) {
+        if (whole[d] < whole[c]) c = d;
+      }
+      whole[c] = whole[c] > INT64_MAX - total[i] ? INT64_MAX : whole[c] + total[i];
+    }
+    double stolen = 0.0;
+    for (const int64_t l : whole) stolen += l < share ? static_cast<double>(share - l) : 0.0;
+    if (stolen * 4.0 <= static_cast<double>(sum)) oversized = 0;
+  }
+
+  Schedule s;
+  s.order.reserve(count);
+  s.tile_time.reserve(count);
+  s.work_offsets.assign(1, 0);
+  s.work_offsets.reserve(count + 1);
+  s.bounds[0] = 0;
+  auto place = [&](int i) {
+    s.order.push_back(i);
+    s.work_offsets.push_back(s.work_offsets.back() + work[i]);
+    s.tile_time.push_back(tile_time[i]);
+  };
   std::array<int64_t, kChunks> load{};
+  int first = 0;  // the first chunk open to the LPT pass
+  if (oversized > 0) {
+    // share < 2^52 here (a total above it is clamped to 2^52), so c * share
+    // and the run's time stay far from overflow.
+    int64_t run_time = 0;  // estimated time of the run before problem i
+    int c = 1;             // the next chunk boundary to place
+    for (int r = 0; r < oversized; ++r) {
+      const int i = by_total[r];
+      for (; c < kChunks && c * share < run_time + total[i]; ++c) {
+        const double x = static_cast<double>(c * share - run_time) / static_cast<double>(total[i]) * work[i];
+        const int j = static_cast<int>(std::floor(x + 0.5));
+        s.bounds[c] = s.work_offsets.back() + std::min(std::max(j, 0), work[i]);
+      }
+      place(i);
+      run_time += total[i];
+    }
+    first = c - 1;
+    load[first] = run_time - first * share;
+  }
   std::array<std::vector<int>, kChunks> members;
-  for (const int i : by_total) {
-    int c = 0;
-    for (int d = 1; d < kChunks; ++d) {
+  for (int r = oversized; r < count; ++r) {
+    const int i = by_total[r];
+    int c = first;
+    for (int d = first + 1; d < kChunks; ++d) {
       if (load[d] < load[c]) c = d;
     }
     load[c] = load[c] > INT64_MAX - total[i] ? INT64_MAX : load[c] + total[i];
     members[c].push_back(i);
   }
-  Schedule s;
-  s.order.reserve(count);
-  s.work_offsets.assign(1, 0);
-  s.work_offsets.reserve(count + 1);
-  s.bounds[0] = 0;
-  for (int c = 0; c < kChunks; ++c) {
+  for (int c = first; c < kChunks; ++c) {
     std::vector<int>& m = members[c];
     std::stable_sort(m.begin(), m.end(), [&](int x, int y) {
       return tile_time[x] != tile_time[y] ? tile_time[x] > tile_time[y] : x < y;
     });
-    for (const int i : m) {
-      s.order.push_back(i);
-      s.work_offsets.push_back(s.work_offsets.back() + work[i]);
-    }
+    for (const int i : m) place(i);
     s.bounds[c + 1] = s.work_offsets.back();
   }
   return s;
@@ -544,6 +605,39 @@ constexpr int kWorkTableMax = 1 << 22;
 constexpr int kTailHalves = GG_TAIL_HALVES;
 constexpr int kTailHalvesMaxPerSlot = 12;
 
+// Idle share of the planned schedule below which no tile is halved.
+constexpr double kTailHalvesMinIdle = 0.02;
+
+// The share of workgroup time the planned schedule leaves idle at its end, by
+// the tile-time estimate: each chunk's work tiles, in claim order, go to
+// whichever of the chunk's workgroups is free first (as its counter hands them
+// out), and the idle share is the time workgroups spend finished while the
+// last one still runs, over grid x the longest chunk.  Halving tail tiles only
+// shortens an end that is ragged: a set of equal tiles that keep every
+// workgroup busy to the same end (one 8192^3 problem: 128 tiles per chunk, 4
+// per workgroup) would only pay the halves' extra B loads (8% measured).
+double planned_idle_share(const Schedule& s, int grid) {
+  constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
+  double busy = 0.0, longest = 0.0;
+  int slots_total = 0;
+  size_t pos = 0;  // the position holding work-tile index t
+  std::vector<double> ends;
+  for (int c = 0; c < kChunks; ++c) {
+    const int slots = c < grid ? (grid - 1 - c) / kChunks + 1 : 0;  // workgroups whose home is chunk c
+    ends.assign(static_cast<size_t>(slots), 0.0);                     // a min-heap of finishing times
+    for (int t = s.bounds[c]; t < s.bounds[c + 1] && slots > 0; ++t) {
+      while (s.work_offsets[pos + 1] <= t) ++pos;
+      std::pop_heap(ends.begin(), ends.end(), std::greater<double>());
+      ends.back() += s.tile_time[pos];
+      std::push_heap(ends.begin(), ends.end(), std::greater<double>());
+      busy += s.tile_time[pos];
+    }
+    for (const double e : ends) longest = std::max(longest, e);
+    slots_total += slots;
+  }
+  return longest > 0.0 && slots_total > 0 ? 1.0 - busy / (slots_total * longest) : 0.0;
+}
+
 // Row of work tiles of work tile `local` in a problem with wtm x wtn of them,
 // in the grouped kernel's order (groups of 4 rows, column by column within a
 // group; gg_kernels.hip, work_tile_position).
@@ -684,7 +778,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds = schedule.bounds;
   if (work_table) {
     const bool halves = kTailHalves > 0 && ggk_work_halves_supported(mode.variant, mode.path) == 1 &&
-                        total_work <= kTailHalvesMaxPerSlot * grid_slots;
+                        total_work <= kTailHalvesMaxPerSlot * grid_slots &&
+                        planned_idle_share(schedule, grid_slots) >= kTailHalvesMinIdle;
     const int bm = config.cta_m * mode.work.tiles_m;
     table.reserve(2 * static_cast<size_t>(total_work) + 4 * GGK_SCHEDULER_CHUNKS * std::max(kTailHalves, 0));
     int index = 0;  // work-tile index of the entry being listed

@@ -167,6 +167,8 @@ def _mapping_sets():
     mm[rng.random(cnt) < 0.3] = 0  # many zero-tile problems
     sets["zeros5000"] = list(zip(mm, rng.integers(1, 300, cnt), rng.integers(0, 50, cnt)))
     sets["one"] = [(1, 1, 1)]
+    # oversized problems cut across chunks: chunk bounds inside problems
+    sets["four_big"] = [(2048, 2048, 64)] * 4 + [(100, 300, 20)] * 5
     return sets
 
 
@@ -310,6 +312,38 @@ def test_host_schedule_is_the_longest_first_plan(torch, config, count):
         say(f"{config} {count} {mode.name}: work shape {shape.tiles_m}x{shape.tiles_n}, {offsets[-1]} work tiles")
         assert (order, offsets, bounds) == want, (config, count, mode)
         ex.close()
+
+
+@pytest.mark.parametrize("name", ["one", "four_equal", "two_big", "one_big_among_many"])
+def test_host_schedule_cuts_oversized_problems(torch, name):
+    """Problems above one chunk's share of the estimated time are cut across consecutive chunks
+    when placing them whole would leave more than a quarter of the work to stealing; the plan
+    equals schedule_plan.py's, and the cut ones are exactly the sets where that rule says so (one
+    problem alone, four equal ones; a single 1.7-share problem among many small ones stays whole)."""
+    rng = np.random.default_rng(11)
+    shapes = {
+        "one": [(4096, 4096, 1024)],
+        "four_equal": [(2048, 2048, 2048)] * 4,
+        "two_big": [(3000, 5000, 700), (2500, 4000, 900)] + [(300, 200, 100)] * 20,
+        "one_big_among_many": [(7000, 4096, 1024)] + [(int(rng.integers(200, 900)), 4096, 1024) for _ in range(40)],
+    }[name]
+    buf = torch.zeros(64, dtype=torch.float32, device="cuda")
+    ptr = buf.data_ptr()
+    problems = [ProblemDesc(m, n, k, ptr, ptr, None, ptr, k, n, n, n) for (m, n, k) in shapes]
+    cfg = KernelConfig.named("128x64x32")
+    prep = api.prepare_problem_set(problems, cfg, SortMode.kByK)
+    ex = GroupedGemmExecutor()
+    assert ex.build(prep, cfg) == 0
+    shape, order, offsets, bounds = ex.schedule()
+    work = [(-(-(-(-p.m // cfg.cta_m)) // shape.tiles_m)) * (-(-(-(-p.n // cfg.cta_n)) // shape.tiles_n))
+            for p in prep.sorted_problems]
+    want = plan_schedule([(p.m, p.n, p.k) for p in prep.sorted_problems], work, cfg.cta_m * shape.tiles_m,
+                         cfg.cta_n * shape.tiles_n, shape.stage_k, False)
+    assert (order, offsets, bounds) == want, name
+    inside = [b for b in bounds[1:-1] if b not in offsets]  # chunk bounds that fall inside a problem
+    say(f"{name}: bounds {bounds}, {len(inside)} inside a problem")
+    assert bool(inside) == (name in ("one", "four_equal", "two_big")), (name, bounds, offsets)
+    ex.close()
 
 
 def test_error_behaviour(torch):

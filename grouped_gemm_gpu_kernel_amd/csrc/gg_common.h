@@ -726,7 +726,9 @@ __device__ __forceinline__ void stage_barrier() {
 // and beta != 0 (src/grouped_gemm.cu:475-479, 616-621).  One fixed rounding
 // sequence -- beta * C rounded, then one fused multiply-add -- so that every
 // work-tile shape, addressing form and path gives the same bits (left to the
-// compiler, the contraction differs between code shapes).
+// compiler, the contraction differs between code shapes).  Where C is not
+// read the callers pass beta = 0 and c = 0, so D is alpha * acc whatever beta
+// holds (an infinite or NaN beta with a null C gives no NaN).
 __device__ __forceinline__ float epilogue_value(float acc, float c, float alpha, float beta) {
   return __builtin_fmaf(alpha, acc, beta * c);
 }

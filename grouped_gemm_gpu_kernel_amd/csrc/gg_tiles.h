@@ -361,7 +361,7 @@ struct MfmaTile {
             floatx4_t out;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              out[e] = epilogue_value(vh[hf][e], cv[chunk % (AHEAD + 1)][i][g][hf][e], p.alpha, p.beta);
+              out[e] = epilogue_value(vh[hf][e], cv[chunk % (AHEAD + 1)][i][g][hf][e], p.alpha, use_c ? p.beta : 0.0f);
             }
             if (r0 + row >= p.m || ncol <= 0) continue;
             const uint32_t off = 4u * ((uint32_t)row * (uint32_t)p.ldd + col);
@@ -448,7 +448,7 @@ struct MfmaTile {
               const int rrow = fm * 32 + 8 * g + lrow;
               floatx4_t out;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[chunk % (AHEAD + 1)][i][fn][g][e], p.alpha, p.beta);
+              for (int e = 0; e < 4; ++e) out[e] = epilogue_value(v[e], cv[chunk % (AHEAD + 1)][i][fn][g][e], p.alpha, use_c ? p.beta : 0.0f);
               if (r0 + rrow >= p.m || ncol <= 0) continue;
               const uint32_t off = 4u * ((uint32_t)rrow * (uint32_t)p.ldd + fn * 32 + lcol);
               if (ncol >= 4) {
@@ -485,7 +485,7 @@ struct MfmaTile {
             g_f32_t* drow = (g_f32_t*)p.d + ((int64_t)row * p.ldd + col);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (e < ncol) drow[e] = epilogue_value(v[e], use_c ? crow[e] : 0.0f, p.alpha, p.beta);
+              if (e < ncol) drow[e] = epilogue_value(v[e], use_c ? crow[e] : 0.0f, p.alpha, use_c ? p.beta : 0.0f);
             }
           }
         }
@@ -583,7 +583,7 @@ struct FmaTile {
 #pragma unroll
       for (int j = 0; j < RN; ++j) {
         const int col = n0 + tn * RN + j;
-        if (col < p.n) dptr[(int64_t)row * p.ldd + col] = epilogue_value(acc[i][j], cv[j], p.alpha, p.beta);
+        if (col < p.n) dptr[(int64_t)row * p.ldd + col] = epilogue_value(acc[i][j], cv[j], p.alpha, use_c ? p.beta : 0.0f);
       }
     }
   }

@@ -346,6 +346,34 @@ def test_host_schedule_cuts_oversized_problems(torch, name):
     ex.close()
 
 
+@pytest.mark.parametrize("config", CONFIGS)
+@pytest.mark.parametrize("mfma", PATHS)
+def test_unread_c_leaves_no_trace(torch, config, mfma):
+    """C is read only when it is given and beta != 0 (src/grouped_gemm.cu:475-479, 616-621): a null C
+    with an infinite or NaN beta, and a NaN-filled C with beta = 0, give D = alpha * A B (the oracle
+    with beta = 0) and no NaN, in every tile class (full, partial rows and columns, a small set)."""
+    rng = np.random.default_rng(3)
+    cfg = KernelConfig.named(config, use_tensor_cores=mfma)
+    shapes = [(300, 270, 100), (64, 64, 16), (129, 40, 33)]
+    for (m, n, k) in shapes:
+        a = O.f32_to_f16(rng.uniform(-1, 1, m * k).astype(np.float32))
+        b = O.f32_to_f16(rng.uniform(-1, 1, k * n).astype(np.float32))
+        want = O.gemm(m, n, k, a, k, b, n, None, n, 1.5, 0.0)
+        da = torch.from_numpy(a.view(np.int16).copy()).cuda()
+        db = torch.from_numpy(b.view(np.int16).copy()).cuda()
+        dc = torch.full((m * n,), float("nan"), device="cuda")
+        for c_ptr, beta in ((None, float("inf")), (None, float("nan")), (dc.data_ptr(), 0.0)):
+            say(f"unread C {config} mfma={mfma} {m}x{n}x{k} c={'set' if c_ptr else 'null'} beta={beta}")
+            dd = torch.full((m * n,), float("nan"), device="cuda")
+            prob = ProblemDesc(m, n, k, da.data_ptr(), db.data_ptr(), c_ptr, dd.data_ptr(), k, n, n, n, 1.5, beta)
+            assert api.run_grouped_gemm_once([prob], SortMode.kByK, cfg) == 0
+            torch.cuda.synchronize()
+            got = dd.cpu().numpy()
+            assert not np.isnan(got).any(), (m, n, k, beta)
+            tol = tolerance(k, np.abs(O.f16_to_f32(a)).max(), np.abs(O.f16_to_f32(b)).max(), 0.0, 1.5, 0.0)
+            assert float(np.abs(got - want[:m * n]).max()) <= tol, (m, n, k, beta)
+
+
 def test_error_behaviour(torch):
     """Status codes of src/grouped_gemm.cu:121-123, 1135-1137, 1147-1152, 1169-1174, 1305-1307."""
     good = KernelConfig.named("128x64x32")

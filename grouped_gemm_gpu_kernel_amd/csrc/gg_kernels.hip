@@ -272,6 +272,38 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       return true;
     };
 
+    // The next index, resolved once this tile's request is back (wave 0:
+    // its chunk's counter value, or a claim of its own once the chunk is
+    // dry), then handed to every wave through LDS and one barrier.  A tile
+    // that is computed does this as soon as its k-loop ends, before its
+    // epilogue: the waves then need no barrier after the epilogue, and those
+    // done first start the next tile's stage loads while the others still
+    // store (the epilogue reads no LDS, and the barrier after the k-loop has
+    // seen every LDS read of this tile).  Slot `parity` was last read before
+    // the previous tile's handover barrier.
+    int next_t = total;
+    bool handed = false;
+    auto hand_over = [&]() {
+      if (wave0) {
+        int next = total;
+        if (chunk >= 0) {
+          next = counted_from(s_schedule, chunk, grid) + __builtin_amdgcn_readfirstlane(got);
+          if (next >= s_schedule[chunk + 1]) {
+            ++visit;
+            next = claim_now(args.state, s_schedule, grid, home, visit, total);
+          }
+        }
+        if (lane == 0) s_claim[parity] = next;
+      }
+      __syncthreads();
+      next_t = __builtin_amdgcn_readfirstlane(s_claim[parity]);
+      handed = true;
+    };
+    auto after_k_loop = [&]() {
+      if (!asked) request();
+      hand_over();
+    };
+
     static_assert(!S::CLASSES || S::TM == 2, "a half of the rows is one row of macro-tiles");
     int prob, local;
     int half = 0;  // 0: the whole work tile; 1, 2: its first or second half of rows
@@ -309,7 +341,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
           }
         }
       } else if (half == 0) {
-        run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request);
+        run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request, after_k_loop);
       } else {
         // One half of the rows (a whole row of macro-tiles), computed as a
         // problem that ends with that half: its tile has at most BM / 2 rows
@@ -319,26 +351,13 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
         const int m0 = wm * G::BM + (half - 1) * (G::BM / 2);
         const int end = m0 + G::BM / 2;
         q.m = end < p.m ? end : p.m;
-        run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request);
+        run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request, after_k_loop);
       }
     }
     if (!asked) request();
+    if (!handed) hand_over();  // nothing computed (or the traced map): hand over now
     if (TRACED) clock_end = wall_clock64();
-
-    if (wave0) {
-      int next = total;
-      if (chunk >= 0) {
-        next = counted_from(s_schedule, chunk, grid) + __builtin_amdgcn_readfirstlane(got);
-        if (next >= s_schedule[chunk + 1]) {
-          ++visit;
-          next = claim_now(args.state, s_schedule, grid, home, visit, total);
-        }
-      }
-      // Slot `parity` was last read before the previous barrier.
-      if (lane == 0) s_claim[parity] = next;
-    }
-    __syncthreads();
-    t = __builtin_amdgcn_readfirstlane(s_claim[parity]);
+    t = next_t;
     parity ^= 1;
   }
 
@@ -371,7 +390,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_single_kernel(gg_device_problem_desc
   if (wtn <= 0 || t >= wtm * wtn) return;
   const int wm = t / wtn;
   const int wn = t - wm * wtn;
-  run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, [] { return false; });
+  run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, [] { return false; }, [] {});
 }
 
 // ---------------------------------------------------------------------------

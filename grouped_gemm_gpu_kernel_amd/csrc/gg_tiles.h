@@ -215,10 +215,12 @@ struct MfmaTile {
     }
   }
 
-  // Computes the work tile at (m0, n0); on_start as in the k-loops.
-  template <bool WIDE, class OnStart>
+  // Computes the work tile at (m0, n0); on_start as in the k-loops, and
+  // after_k_loop() once by every thread when the k-loop is over (no LDS read
+  // of this tile follows it: the epilogue works from registers).
+  template <bool WIDE, class OnStart, class AfterKLoop>
   __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                             OnStart&& on_start) {
+                                             OnStart&& on_start, AfterKLoop&& after_k_loop) {
     const int tid = opaque_tid();
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -244,6 +246,7 @@ struct MfmaTile {
     } else {
       run_k_loop_dma<G>(p, m0, n0, lds, compute, on_start);
     }
+    after_k_loop();
 
     if (!live) return;
     store_tile<WIDE>(p, m0 + wm * WM, n0 + wn * WN, lane, acc);
@@ -544,10 +547,11 @@ struct FmaTile {
     }
   }
 
-  // Computes the work tile at (m0, n0); on_start as in the k-loops.
-  template <bool WIDE, class OnStart>
+  // Computes the work tile at (m0, n0); on_start and after_k_loop as in
+  // MfmaTile::run.
+  template <bool WIDE, class OnStart, class AfterKLoop>
   __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                             OnStart&& on_start) {
+                                             OnStart&& on_start, AfterKLoop&& after_k_loop) {
     const int tid = threadIdx.x;
     const int tm = tid >> 4;
     const int tn = tid & 15;
@@ -565,6 +569,7 @@ struct FmaTile {
       if (active) compute_stage(stage, p.k - kt * G::BK, tm, tn, acc);
       ++kt;
     }, on_start);
+    after_k_loop();
 
     if (!active) return;
     const bool use_c = p.c != nullptr && p.beta != 0.0f;
@@ -612,25 +617,25 @@ struct KernelLds<S, true> {
 // Computes the work tile at (m0, n0): in the edge class its extent inside the
 // problem selects (KernelShape::CLASSES), else in the kernel's own form.  The
 // class is uniform across the workgroup (scalar descriptor and origin).
-template <class S, int PATH, bool WIDE, class OnStart>
+template <class S, int PATH, bool WIDE, class OnStart, class AfterKLoop>
 __device__ __forceinline__ void run_work_tile(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                              OnStart&& on_start) {
+                                              OnStart&& on_start, AfterKLoop&& after_k_loop) {
   if constexpr (PATH == GGK_PATH_MFMA && !WIDE && S::CLASSES) {
     const bool rows = p.m - m0 <= S::G::BM / 2;
     const bool cols = p.n - n0 <= S::G::BN / 2;
     // The full form first: its code then follows the dispatch as it would
     // without the edge classes.
     if (__builtin_expect(!rows && !cols, 1)) {
-      TileFor<S, PATH>::type::template run<false>(p, m0, n0, lds, on_start);
+      TileFor<S, PATH>::type::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
     } else if (!cols) {
-      MfmaTile<typename S::GR, S::WAVE_M_R>::template run<false>(p, m0, n0, lds, on_start);
+      MfmaTile<typename S::GR, S::WAVE_M_R>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
     } else if (!rows) {
-      MfmaTile<typename S::GC, S::WAVE_M_C>::template run<false>(p, m0, n0, lds, on_start);
+      MfmaTile<typename S::GC, S::WAVE_M_C>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
     } else {
-      MfmaTile<typename S::GRC, S::WAVE_M_RC>::template run<false>(p, m0, n0, lds, on_start);
+      MfmaTile<typename S::GRC, S::WAVE_M_RC>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
     }
   } else {
-    TileFor<S, PATH>::type::template run<WIDE>(p, m0, n0, lds, on_start);
+    TileFor<S, PATH>::type::template run<WIDE>(p, m0, n0, lds, on_start, after_k_loop);
   }
 }
 

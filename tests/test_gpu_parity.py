@@ -471,6 +471,88 @@ def test_padded_leading_dimensions(torch):
                 assert np.isnan(got[:, n:]).all(), "padding columns of D were written"
 
 
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_random_sets_against_oracle(torch, seed):
+    """Seeded random problem sets mixing everything at once: sizes 0..320 (K 0..400, odd and even),
+    padded leading dimensions, matrices at 2-byte offsets, alpha and beta of either sign or zero, C
+    null on some problems.  For every configuration and both paths: the four sort modes and the
+    per-problem baseline give bit-identical D, D matches the oracle within the bound, and the
+    padding columns of D stay NaN."""
+    rng = np.random.default_rng(100 + seed)
+    count = 24
+    probs_host, keep = [], []
+    for i in range(count):
+        m, n = (int(x) for x in rng.integers(0, 321, 2))
+        k = int(rng.integers(0, 401))
+        if rng.random() < 0.1:
+            m = 0
+        pa, pb, pc, pd = (int(x) for x in rng.integers(0, 9, 4))
+        off = int(rng.integers(0, 2))
+        lda, ldb, ldc, ldd = max(1, k + pa), max(1, n + pb), max(1, n + pc), max(1, n + pd)
+        alpha = float(rng.choice([1.0, -0.75, 1.5]))
+        beta = float(rng.choice([0.0, 0.5, -1.25]))
+        with_c = bool(rng.random() < 0.8)
+        a = O.f32_to_f16(rng.uniform(-1, 1, max(1, m * lda) + off).astype(np.float32))
+        b = O.f32_to_f16(rng.uniform(-1, 1, max(1, k * ldb) + off).astype(np.float32))
+        c = rng.uniform(-1, 1, max(1, m * ldc)).astype(np.float32)
+        da = torch.from_numpy(a.view(np.int16).copy()).cuda()
+        db = torch.from_numpy(b.view(np.int16).copy()).cuda()
+        dc = torch.from_numpy(c.copy()).cuda()
+        dd = torch.full((max(1, m * ldd),), float("nan"), device="cuda")
+        keep.append((da, db, dc, dd))
+        probs_host.append((m, n, k, a[off:], b[off:], c if with_c else None, lda, ldb, ldc, ldd, alpha, beta))
+        probs_host[-1] = probs_host[-1] + (ProblemDesc(m, n, k, da.data_ptr() + 2 * off, db.data_ptr() + 2 * off,
+                                                       dc.data_ptr() if with_c else None, dd.data_ptr(),
+                                                       lda, ldb, ldc, ldd, alpha, beta),)
+    problems = [h[-1] for h in probs_host]
+    wants = []
+    for (m, n, k, a, b, c, lda, ldb, ldc, ldd, alpha, beta, _) in probs_host:
+        if m > 0 and n > 0:
+            # The reference reads C only when given with beta != 0.
+            c_used = c if (c is not None and beta != 0.0) else None
+            wants.append(O.gemm(m, n, k, a, lda, b, ldb, c_used, ldc, alpha, beta if c_used is not None else 0.0,
+                                ldd=ldd).reshape(m, ldd))
+        else:
+            wants.append(None)
+
+    def outputs():
+        torch.cuda.synchronize()
+        return [kp[3].cpu().numpy() for kp in keep]
+
+    for config in CONFIGS:
+        for mfma in PATHS:
+            cfg = KernelConfig.named(config, use_tensor_cores=mfma)
+            ref = None
+            for mode in list(SortMode) + ["baseline"]:
+                say(f"random set seed={seed} {config} mfma={mfma} mode={mode}")
+                for kp in keep:
+                    kp[3].fill_(float("nan"))
+                if mode == "baseline":
+                    assert api.run_baseline_per_problem(problems, cfg) == 0
+                else:
+                    assert api.run_grouped_gemm_once(problems, mode, cfg) == 0
+                outs = outputs()
+                if ref is None:
+                    for i, (h, got, want) in enumerate(zip(probs_host, outs, wants)):
+                        m, n, k, a, b, c, lda, ldb, ldc, ldd, alpha, beta, _ = h
+                        if want is None:
+                            assert np.isnan(got).all(), (seed, config, mfma, i, "empty problem written")
+                            continue
+                        g = got[:m * ldd].reshape(m, ldd)
+                        amax = np.abs(O.f16_to_f32(a[:max(1, m * lda)])).max() if k > 0 else 0.0
+                        bmax = np.abs(O.f16_to_f32(b[:max(1, k * ldb)])).max() if k > 0 else 0.0
+                        cmax = float(np.abs(c).max()) if c is not None and beta != 0.0 else 0.0
+                        tol = tolerance(k, amax, bmax, cmax, alpha, beta)
+                        assert not np.isnan(g[:, :n]).any(), (seed, config, mfma, i, "unwritten elements")
+                        assert float(np.abs(g[:, :n] - want[:, :n]).max()) <= tol, (seed, config, mfma, i, m, n, k)
+                        assert np.isnan(g[:, n:]).all(), (seed, config, mfma, i, "padding columns written")
+                    ref = outs
+                else:
+                    for i in range(count):
+                        assert np.array_equal(np.nan_to_num(outs[i], nan=7.0).view(np.uint32),
+                                              np.nan_to_num(ref[i], nan=7.0).view(np.uint32)), (seed, config, mfma, mode, i)
+
+
 def test_matrix_end_values(torch):
     """The last value of A and of B (the dword that holds it can reach 2 bytes past the matrix and then
     reads as zero; the loader puts the value back exactly where that happens: odd K for A, odd N for B)

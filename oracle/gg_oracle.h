@@ -5,7 +5,7 @@
  * reference implementation (Intersect-Suo/Grouped_GEMM_gpu_kernel) computes on
  * the grouped-GEMM path, so that the HIP library can be checked against it.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
- * it, and only as the checker or the timed CPU baseline.  The product library
+ * it, and only as the expected answer or the timed CPU baseline.  The product library
  * (grouped_gemm_gpu_kernel_amd) never links, loads or calls it.
  *
  * Every function names the reference file:line it follows.  How each one is

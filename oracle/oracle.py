@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so, built by `make -C oracle`).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
-bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.  The
+bench.py's cpu_baseline leg, as the expected answer or the timed CPU baseline.  The
 product package never imports it.  Function semantics and reference citations
 are in oracle/gg_oracle.h.
 """

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/gg_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/gg_oracle.c) before its answers are trusted.
 
 Each oracle function is checked against something other than its own formula:
 the C++ standard's mt19937 known answer, libstdc++ itself, the reference's

@@ -2,8 +2,8 @@
  * gg_oracle.c -- CPU oracle for the grouped FP16 GEMM path.
  *
  * TEST INFRASTRUCTURE ONLY: a plain-C restatement of the reference's
- * grouped-GEMM semantics, the expected answer for tests/ and
- * __graft_entry__.smoke() and as the timed CPU baseline in bench.py.  The
+ * grouped-GEMM semantics: the expected answer for tests/ and
+ * __graft_entry__.smoke(), and the timed CPU baseline in bench.py.  The
  * product library never links or calls it.
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).  The FP32 GEMM

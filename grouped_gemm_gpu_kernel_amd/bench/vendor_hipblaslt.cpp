@@ -1,8 +1,9 @@
 // vendor_hipblaslt -- the vendor comparison point for the grouped GEMM: a
 // problem list (row-major fp16 A/B, fp32 C/D, fp32 accumulate, per-problem
-// alpha/beta) run by hipBLASLt as one hipblaslt_ext::GroupedGemm and as one
-// hipblasLtMatmul per problem, next to this library's grouped launch on the
-// same buffers.  This is the taskbook's library baseline option
+// alpha/beta) run by hipBLASLt as one hipblaslt_ext::GroupedGemm, as one
+// hipblasLtMatmul per problem and, for sets of equal problems at evenly spaced
+// addresses, as one strided-batched hipblasLtMatmul, next to this library's
+// grouped launch on the same buffers.  This is the taskbook's library baseline option
 // (taskbook_grouped_gemm.md:147-159); it is measured beside the library and is
 // not part of it.
 //
@@ -326,6 +327,48 @@ int per_problem_run(Vendor* v) {
   return 0;
 }
 
+// Strided-batched form, for sets whose problems all have the same shape,
+// leading dimensions and scalars and sit at evenly spaced addresses (uniform
+// sets such as 64 x 2048^3): one hipblasLtMatmul over the whole batch, the
+// best of up to max_algos heuristic candidates.  Returns false (and a reason)
+// when the set is not uniform.
+struct Batched {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr, ld = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  std::string solution;
+  ~Batched() {
+    if (la) hipblasLtMatrixLayoutDestroy(la);
+    if (lb) hipblasLtMatrixLayoutDestroy(lb);
+    if (lc) hipblasLtMatrixLayoutDestroy(lc);
+    if (ld) hipblasLtMatrixLayoutDestroy(ld);
+    if (desc) hipblasLtMatmulDescDestroy(desc);
+  }
+};
+
+bool uniform_set(const std::vector<gg::ProblemDesc>& ps, std::string* why) {
+  if (ps.size() < 2) return *why = "fewer than two problems", false;
+  const gg::ProblemDesc& p0 = ps[0];
+  if (p0.m <= 0 || p0.n <= 0 || p0.k <= 0) return *why = "empty problem", false;
+  auto gap = [](const void* x, const void* y) {
+    return reinterpret_cast<const char*>(y) - reinterpret_cast<const char*>(x);
+  };
+  const bool with_c = p0.c != nullptr && p0.beta != 0.0f;
+  for (size_t i = 1; i < ps.size(); ++i) {
+    const gg::ProblemDesc& p = ps[i];
+    const gg::ProblemDesc& q = ps[i - 1];
+    if (p.m != p0.m || p.n != p0.n || p.k != p0.k || p.lda != p0.lda || p.ldb != p0.ldb || p.ldc != p0.ldc ||
+        p.ldd != p0.ldd || p.alpha != p0.alpha || p.beta != p0.beta || (p.c != nullptr) != (p0.c != nullptr)) {
+      return *why = "problems differ", false;
+    }
+    if (gap(q.a, p.a) != gap(p0.a, ps[1].a) || gap(q.b, p.b) != gap(p0.b, ps[1].b) ||
+        gap(q.d, p.d) != gap(p0.d, ps[1].d) || (with_c && gap(q.c, p.c) != gap(p0.c, ps[1].c))) {
+      return *why = "uneven spacing", false;
+    }
+  }
+  return true;
+}
+
 struct Result {
   std::string error, solution;
   float ms = -1.0f;
@@ -503,11 +546,87 @@ int main(int argc, char** argv) {
     }
   }
 
+  Result batched;  // strided-batched form (uniform sets only)
+  if (ready) {
+    std::string why;
+    if (!uniform_set(theirs, &why)) {
+      batched.error = "not a uniform set: " + why;
+    } else {
+      try {
+        const gg::ProblemDesc& p = theirs[0];
+        const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+        const int64_t count = static_cast<int64_t>(theirs.size());
+        auto stride = [](const void* x, const void* y, int64_t elem) {
+          return (reinterpret_cast<const char*>(y) - reinterpret_cast<const char*>(x)) / elem;
+        };
+        const int64_t sa = stride(theirs[0].b, theirs[1].b, 2), sb = stride(theirs[0].a, theirs[1].a, 2);
+        const int64_t sd = stride(theirs[0].d, theirs[1].d, 4);
+        const int64_t sc = reads_c ? stride(theirs[0].c, theirs[1].c, 4) : sd;
+        Batched bt;
+        hipblasLtMatmulDescCreate(&bt.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+        const hipblasOperation_t op = HIPBLAS_OP_N;
+        hipblasLtMatmulDescSetAttribute(bt.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op));
+        hipblasLtMatmulDescSetAttribute(bt.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op));
+        hipblasLtMatrixLayoutCreate(&bt.la, HIP_R_16F, p.n, p.k, p.ldb);
+        hipblasLtMatrixLayoutCreate(&bt.lb, HIP_R_16F, p.k, p.m, p.lda);
+        hipblasLtMatrixLayoutCreate(&bt.lc, HIP_R_32F, p.n, p.m, reads_c ? p.ldc : p.ldd);
+        hipblasLtMatrixLayoutCreate(&bt.ld, HIP_R_32F, p.n, p.m, p.ldd);
+        const int32_t batch = static_cast<int32_t>(count);
+        for (auto [layout, st] : {std::pair{bt.la, sa}, std::pair{bt.lb, sb}, std::pair{bt.lc, sc}, std::pair{bt.ld, sd}}) {
+          hipblasLtMatrixLayoutSetAttribute(layout, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &batch, sizeof(batch));
+          hipblasLtMatrixLayoutSetAttribute(layout, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st, sizeof(st));
+        }
+        hipblasLtMatmulPreference_t pref = nullptr;
+        hipblasLtMatmulPreferenceCreate(&pref);
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &v.workspace_bytes,
+                                              sizeof(v.workspace_bytes));
+        std::vector<hipblasLtMatmulHeuristicResult_t> cand(std::max(1, max_algos));
+        int returned = 0;
+        const float alpha = p.alpha, beta = reads_c ? p.beta : 0.0f;
+        const void* c_ptr = reads_c ? static_cast<const void*>(p.c) : p.d;
+        if (hipblasLtMatmulAlgoGetHeuristic(v.handle, bt.desc, bt.la, bt.lb, bt.lc, bt.ld, pref,
+                                            static_cast<int>(cand.size()), cand.data(), &returned) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            returned == 0) {
+          batched.error = "no strided-batched algorithm";
+        } else {
+          auto run_with = [&](const hipblasLtMatmulAlgo_t& algo) {
+            return hipblasLtMatmul(v.handle, bt.desc, &alpha, p.b, bt.la, p.a, bt.lb, &beta, c_ptr, bt.lc, p.d, bt.ld,
+                                   &algo, v.workspace, v.workspace_bytes, nullptr) == HIPBLAS_STATUS_SUCCESS
+                       ? 0
+                       : 1;
+          };
+          int best = -1;
+          for (int i = 0; i < returned; ++i) {
+            const float ms = time_ms(std::max(1, std::min(steps, 10)), 2, [&] { return run_with(cand[i].algo); });
+            ++batched.candidates;
+            if (ms > 0 && (best < 0 || ms < batched.ms)) best = i, batched.ms = ms;
+          }
+          if (best < 0) {
+            batched.error = "no strided-batched algorithm could be run";
+          } else {
+            bt.algo = cand[best].algo;
+            batched.solution = hipblaslt_ext::getSolutionNameFromAlgo(v.handle, bt.algo);
+            HIP_OK(ggk_fill_f32(pools.d_vendor, std::max<int64_t>(pools.d_n, 1), NAN, nullptr));
+            if (run_with(bt.algo) != 0) batched.error = "strided-batched hipblasLtMatmul failed";
+            HIP_OK(hipDeviceSynchronize());
+            if (batched.error.empty() && check) batched.check = compare(spec, pools, skipped), batched.checked = true;
+            if (batched.error.empty()) batched.ms = time_ms(steps, warmup, [&] { return run_with(bt.algo); });
+          }
+        }
+        hipblasLtMatmulPreferenceDestroy(pref);
+      } catch (const std::exception& e) {
+        batched.error = std::string("hipBLASLt raised: ") + e.what();
+      }
+    }
+  }
+
   std::printf("{\"problems\": %zu, \"gflop\": %.3f, \"library\": {\"mode\": \"%s\", \"kernel_ms\": %g, \"tflops\": %g}, "
-              "\"vendor\": [%s, %s]}\n",
+              "\"vendor\": [%s, %s, %s]}\n",
               spec.m.size(), flops / 1e9, gg::sort_mode_name(static_cast<gg::SortMode>(sort_mode)), ours_ms,
               flops / (ours_ms * 1e-3) / 1e12, result_json("hipblaslt_grouped", grouped, flops).c_str(),
-              result_json("hipblaslt_per_problem", singles, flops).c_str());
+              result_json("hipblaslt_per_problem", singles, flops).c_str(),
+              result_json("hipblaslt_strided_batched", batched, flops).c_str());
   HIP_OK(hipFree(pools.a));
   HIP_OK(hipFree(pools.b));
   HIP_OK(hipFree(pools.c));

@@ -58,10 +58,23 @@ def _assert_passes(row):
 def test_vendor_matches_library_on_edge_shapes(c_dist):
     res = vendor.run(_spec(TEST_SHAPES, c_dist=c_dist), steps=3, warmup=1)
     print(res, flush=True)
-    grouped, per_problem = res["vendor"]
+    grouped, per_problem, batched = res["vendor"]
     _assert_passes(grouped)
     _assert_passes(per_problem)
+    assert "not a uniform set" in batched.get("error", ""), batched
     assert res["library"]["kernel_ms"] > 0
+
+
+@pytest.mark.gpu
+def test_vendor_strided_batched_on_a_uniform_set():
+    # Equal problems at evenly spaced addresses also run as one strided-batched hipblasLtMatmul.
+    m, n, k = (np.full(4, x) for x in (256, 384, 160))
+    spec = custom_spec("vendor-batched", m, n, k, alpha=np.full(4, 1.25), beta=np.full(4, 0.5))
+    res = vendor.run(spec, steps=3, warmup=1)
+    print(res, flush=True)
+    grouped, per_problem, batched = res["vendor"]
+    _assert_passes(per_problem)
+    _assert_passes(batched)
 
 
 @pytest.mark.gpu
@@ -70,11 +83,11 @@ def test_vendor_on_plumbing_workload_and_unsupported_set():
     # the vendor's grouped GEMM without an algorithm: that is reported, never a wrong answer.
     res = vendor.run(make_spec("plumbing16"), steps=3, warmup=1)
     print(res, flush=True)
-    grouped, per_problem = res["vendor"]
+    grouped, per_problem, _ = res["vendor"]
     assert "error" in grouped or grouped["check_vs_library"]["pass"], grouped
     _assert_passes(per_problem)
     res = vendor.run(_spec([(64, 64, 64), (1, 1, 1)]), steps=2, warmup=1)
     print(res, flush=True)
-    grouped, per_problem = res["vendor"]
+    grouped, per_problem, _ = res["vendor"]
     assert "error" in grouped or grouped["check_vs_library"]["pass"], grouped
     _assert_passes(per_problem)

@@ -31,7 +31,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--clock-warmup", type=float, default=0.3,
-                    help="seconds of untimed launches before the first timed mode (0.1 s before the others)")
+                    help="seconds of untimed launches before the first timed mode (at most 0.1 s before every other timed leg)")
     ap.add_argument("--workload", default=None,
                     choices=["plumbing16", "mixed512", "dense64", "moe64", "longtail4096"],
                     help="default mixed512 (summaries: the workload profiled, for useful-work ratios)")
@@ -103,6 +103,19 @@ def time_runs(torch, fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / steps
 
 
+def warm_clock(torch, fn, seconds: float) -> None:
+    """Untimed calls of fn for `seconds`: the GPU lowers its clock within milliseconds of idling (a
+    build, a traced run, a host copy) and takes tens of milliseconds of load to raise it again, so
+    each timed stretch starts after a stretch of its own launches."""
+    deadline = time.perf_counter() + seconds
+    while time.perf_counter() < deadline:
+        for _ in range(20):
+            st = fn()
+            if isinstance(st, int) and st != 0:
+                raise RuntimeError(f"warm-up run: hipError_t {st}")
+        torch.cuda.synchronize()
+
+
 def timed_prepare_and_build(probs, cfg, mode):
     """(executor, ms) for prepare_problem_set + build through the C-ABI, timed on the host."""
     import ctypes
@@ -126,23 +139,28 @@ def timed_prepare_and_build(probs, cfg, mode):
     return ex, ms
 
 
-def measured_tail_idle(torch, ex) -> float:
+def measured_tail_idle(torch, ex, runs: int = 3) -> float:
     """Share of workgroup time spent idle after finishing its last tile while others still run:
-    sum_w (T_end - end_w) / (W * (T_end - T_start)), from per-workgroup wall clocks."""
+    sum_w (T_end - end_w) / (W * (T_end - T_start)), from per-workgroup wall clocks; the median
+    over `runs` back-to-back traced launches (one launch now and then has a workgroup that starts
+    late, which reads as several percent of idle)."""
+    import statistics
+
     grid = ex.grid_ctas()
     clock = torch.zeros(2 * grid, dtype=torch.int64, device="cuda")
-    st = ex.run_traced(0, clock.data_ptr())
-    if st != 0:
-        raise RuntimeError(f"traced run hipError_t {st}")
-    torch.cuda.synchronize()
-    c = clock.cpu().numpy().reshape(grid, 2).astype("float64")
-    t0, t1 = c[:, 0].min(), c[:, 1].max()
-    if t1 <= t0:
-        return 0.0
-    return float(((t1 - c[:, 1]).sum()) / (grid * (t1 - t0)))
+    shares = []
+    for _ in range(runs):
+        st = ex.run_traced(0, clock.data_ptr())
+        if st != 0:
+            raise RuntimeError(f"traced run hipError_t {st}")
+        torch.cuda.synchronize()
+        c = clock.cpu().numpy().reshape(grid, 2).astype("float64")
+        t0, t1 = c[:, 0].min(), c[:, 1].max()
+        shares.append(float(((t1 - c[:, 1]).sum()) / (grid * (t1 - t0))) if t1 > t0 else 0.0)
+    return statistics.median(shares)
 
 
-def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int) -> dict:
+def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int, warm_seconds: float) -> dict:
     """The same workload through the torch binding: GroupedGemmPlan.run() (device time, events on
     the launch stream) and one-shot run_grouped_gemm (host wall time per call: prepare, upload,
     launch, wait, release)."""
@@ -150,6 +168,7 @@ def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int) -> dict
 
     a, b, c, d, alpha, beta = dw.tensors()
     plan = torch_ops.GroupedGemmPlan(a, b, c if dw.has_c else None, d, alpha, beta, sort_mode=mode, config=cfg)
+    warm_clock(torch, lambda: plan.run(stream), warm_seconds)
     plan_ms = time_runs(torch, lambda: plan.run(stream), steps, warmup)
     plan.close()
     calls = 5
@@ -163,7 +182,7 @@ def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int) -> dict
     return out
 
 
-def moe_device_prepare(torch, dw, spec, cfg, mode, stream, steps: int, warmup: int):
+def moe_device_prepare(torch, dw, spec, cfg, mode, stream, steps: int, warmup: int, warm_seconds: float):
     """A group whose problems share n and k and read no C (moe64) through the device-side prepare:
     the expert rows of A stacked into one [T, k] tensor, B as [E, k, n], the int32 counts on the
     GPU; prepare kernel + grouped launch per run (device time, events on the launch stream), next
@@ -187,6 +206,7 @@ def moe_device_prepare(torch, dw, spec, cfg, mode, stream, steps: int, warmup: i
     counts = torch.from_numpy(rows.astype(np.int32)).cuda()
     plan = torch_ops.MoeGroupedGemmPlan(a, b, d, None, float(spec.alpha[0]), float(spec.beta[0]), sort_mode=mode,
                                         config=cfg)
+    warm_clock(torch, lambda: plan.run(counts, stream), warm_seconds)
     ms = time_runs(torch, lambda: plan.run(counts, stream), steps, warmup)
     status = plan.status()
     plan.close()
@@ -323,13 +343,14 @@ def _dispatches(d: Path):
 
 def _segments(dispatches, kernel_filter: str, names, last: int):
     """{(kernel, segment name): {metric: [values]}} for the kernels matching kernel_filter.  With
-    names, the dispatches are cut into segments at each traced grouped-kernel dispatch (bench.py
-    makes one after each sort mode's timed runs, so segment i holds mode i's clock warm-up, warm-up
-    and timed runs) and only the last `last` dispatches of each segment count (0: all of them);
-    dispatches after the last cut form a segment named "after".  Without names: one segment "all"."""
+    names, the dispatches are cut into segments at each run of traced grouped-kernel dispatches
+    (bench.py makes them after each sort mode's timed runs, so segment i holds mode i's clock
+    warm-up, warm-up and timed runs) and only the last `last` dispatches of each segment count (0:
+    all of them); dispatches after the last cut form a segment named "after".  Without names: one
+    segment "all"."""
     import re
     pat, cut = re.compile(kernel_filter), re.compile(TRACED_KERNEL)
-    segs, current, seg = {}, {}, 0
+    segs, current, seg, in_cut = {}, {}, 0, False
 
     def close(name):
         for kname, rows in current.items():
@@ -341,10 +362,12 @@ def _segments(dispatches, kernel_filter: str, names, last: int):
 
     for _, kname, metrics in dispatches:
         if names and cut.search(kname):
-            close(names[seg] if seg < len(names) else f"segment{seg}")
-            current, seg = {}, seg + 1
+            if not in_cut:
+                close(names[seg] if seg < len(names) else f"segment{seg}")
+                current, seg, in_cut = {}, seg + 1, True
         elif pat.search(kname):
             current.setdefault(kname, []).append(metrics)
+            in_cut = False
     close("after" if names else "all")
     return segs
 
@@ -539,9 +562,8 @@ def main() -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     # Every mode's executor is built first (host work), then each is timed right after an untimed
-    # stretch of its own launches: the GPU lowers its clock within milliseconds of idling (a build,
-    # a traced run, a host copy) and takes tens of milliseconds of load to raise it again, which
-    # otherwise shows up as a 5-10% slower mode depending only on its place in the order.
+    # stretch of its own launches (warm_clock); without it a mode reads 5-10% slower depending only
+    # on its place in the order.
     # prep_ms is the reference benchmark's span (bench/benchmark_grouped_gemm.cu:622-632):
     # prepare_problem_set + GroupedGemmExecutor::build, here the two C calls on a problem array
     # converted from Python beforehand.  The first build in a process also queries the device and
@@ -553,19 +575,11 @@ def main() -> int:
         prep = api.prepare_problem_set(probs, cfg, mode)
         built.append((mode, prep, ex, prep_ms))
 
-    def clock_warmup(ex, seconds: float) -> None:
-        deadline = time.perf_counter() + seconds
-        while time.perf_counter() < deadline:
-            for _ in range(20):
-                if ex.run(stream) != 0:
-                    raise RuntimeError("warm-up run failed")
-            torch.cuda.synchronize()
-
     timed = []
     for i, (mode, prep, ex, prep_ms) in enumerate(built):
-        clock_warmup(ex, args.clock_warmup if i == 0 else min(args.clock_warmup, 0.1))
+        warm_clock(torch, lambda: ex.run(stream), args.clock_warmup if i == 0 else min(args.clock_warmup, 0.1))
         ms = time_runs(torch, lambda: ex.run(stream), args.steps, args.warmup)
-        # The traced run right after a mode's timed runs also marks, in a profiler's dispatch list,
+        # The traced runs right after a mode's timed runs also mark, in a profiler's dispatch list,
         # where that mode's runs end (--profile-summary / --traffic-summary --modes-of-segments).
         timed.append((ms, measured_tail_idle(torch, ex)))
     for (mode, prep, ex, prep_ms), (ms, tail_idle) in zip(built, timed):
@@ -584,6 +598,7 @@ def main() -> int:
     baseline = None
     if not args.no_baseline:
         bsteps = max(1, min(args.steps, 20))
+        warm_clock(torch, lambda: api.run_baseline_per_problem(probs, cfg, stream), min(args.clock_warmup, 0.1))
         bms = time_runs(torch, lambda: api.run_baseline_per_problem(probs, cfg, stream), bsteps, 2)
         baseline = {"mode": "baseline_per_problem", "kernel_ms": round(bms, 4),
                     "tflops": round(flops / (bms * 1e-3) / 1e12, 3),
@@ -591,12 +606,13 @@ def main() -> int:
         print(f"# {baseline}", file=sys.stderr, flush=True)
 
     best_mode = next(m for m in modes if api.sort_mode_name(m) == best[0]["mode"])
-    moe_device = None if (args.fma or args.no_moe_device) else moe_device_prepare(torch, dw, spec, cfg, best_mode, stream, args.steps,
-                                                          args.warmup)
+    warm_s = min(args.clock_warmup, 0.1)
+    moe_device = None if (args.fma or args.no_moe_device) else moe_device_prepare(
+        torch, dw, spec, cfg, best_mode, stream, args.steps, args.warmup, warm_s)
     vendor_rows = None if (args.no_vendor or args.fma) else vendor_baseline(spec, config_name, int(best_mode),
                                                                             args.steps, args.warmup)
     torch_op = None if args.no_torch_op else torch_binding(torch, dw, cfg, best_mode, stream, args.steps,
-                                                          args.warmup)
+                                                          args.warmup, warm_s)
     cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds, args.cpu_full)
 
     row, ms = best

@@ -48,15 +48,18 @@ def write_trace(folder: Path, rows):
             t += int(us * 1000) + 500
 
 
-def dispatch_rows(mode_values, after=()):
+def dispatch_rows(mode_values, after=(), traced=3):
+    """bench.py's dispatch order: each mode's untraced runs, then `traced` traced runs (the
+    measured tail idle is a median over several)."""
     rows = [(FILL, 7.0)]
     for vals in mode_values:
-        rows += [(UNTRACED, v) for v in vals] + [(TRACED, 1e9)]
+        rows += [(UNTRACED, v) for v in vals] + [(TRACED, 1e9)] * traced
     return rows + [(UNTRACED, v) for v in after]
 
 
-def test_segments_split_at_traced_dispatches(bench, tmp_path):
-    rows = dispatch_rows([[100.0, 10.0, 20.0], [50.0, 30.0, 40.0]], after=[999.0])
+@pytest.mark.parametrize("traced", [1, 3])
+def test_segments_split_at_traced_dispatches(bench, tmp_path, traced):
+    rows = dispatch_rows([[100.0, 10.0, 20.0], [50.0, 30.0, 40.0]], after=[999.0], traced=traced)
     write_trace(tmp_path / "t", rows)
     segs = bench._segments(bench._dispatches(tmp_path / "t"), r"gg_grouped_kernel<\d+,\s*\d+,\s*false",
                            ["none", "sort_by_k"], last=2)

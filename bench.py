@@ -6,7 +6,7 @@ macro-tile 128x64x32), for all four sort modes, next to the per-problem-launch b
 tail share and the measured tail idle.  A step is one executor.run() over the whole set with every
 operand already resident in HBM.  `value` is the best sort mode's throughput.
 
-Prints one JSON line.  --gpus above 1 exits: this build measures one GPU.
+Prints one JSON line.  --gpus above 1 exits: the bench measures one GPU.
 """
 from __future__ import annotations
 

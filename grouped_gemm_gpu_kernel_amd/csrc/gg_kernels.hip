@@ -22,7 +22,7 @@
 #include "gg_tiles.h"
 #include "grouped_gemm_amd_kernels.h"
 
-// Compiler resource table of this build (generated from the compiler's
+// Compiler resource table of the compiled kernels (generated from the compiler's
 // resource-usage report; see gg_resources.cpp).
 extern "C" int gg_compiler_resources(int kind, int variant, int path, int* vgprs, int* agprs,
                                      int* sgprs, int* scratch, int* waves_per_simd, int* lds);

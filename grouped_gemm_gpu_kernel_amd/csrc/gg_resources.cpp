@@ -1,4 +1,4 @@
-// gg_resources.cpp -- per-kernel register and LDS figures of this build.
+// gg_resources.cpp -- per-kernel register and LDS figures of the compiled kernels.
 //
 // The table comes from the compiler's resource-usage report for
 // gg_kernels.hip (VGPRs, AGPRs, SGPRs, scratch, waves per SIMD, LDS), which the

@@ -110,7 +110,7 @@ typedef struct ggk_device_info {
 } ggk_device_info;
 
 /* Resources of one compiled kernel.  vgprs/agprs/sgprs/scratch come from the
- * compiler's resource report of this build; num_regs, lds_static, local_bytes
+ * compiler's resource report of the library as compiled; num_regs, lds_static, local_bytes
  * and max_threads from hipFuncGetAttributes. */
 typedef struct ggk_kernel_resources {
   int vgprs;

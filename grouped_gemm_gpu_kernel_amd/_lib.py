@@ -24,6 +24,7 @@ GGK_VARIANT_128x64x32 = 1
 GGK_VARIANT_64x128x32 = 2
 GGK_VARIANT_128x64x32_SMALL = 3  # 128x64x32 on 128 x 128 work tiles (launches with few work tiles)
 GGK_VARIANT_64x128x32_SMALL = 4  # 64x128x32 on 128 x 128 work tiles
+GGK_VARIANT_64x64x16_SMALL = 5  # 64x64x16 on 128 x 128 work tiles
 GGK_PATH_FMA = 0
 GGK_PATH_MFMA = 1
 GGK_KERNEL_GROUPED = 0

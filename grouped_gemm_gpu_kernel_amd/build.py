@@ -123,8 +123,8 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), c
         fut_moe.result()
 
     rows = parse_resource_report(report)
-    if len(rows) != 20:
-        raise RuntimeError(f"expected 20 kernel resource rows, parsed {len(rows)}")
+    if len(rows) != 24:
+        raise RuntimeError(f"expected 24 kernel resource rows, parsed {len(rows)}")
     table = "".join("    {%d, %d, %d, %d, %d, %d, %d, %d, %d},\n" % r for r in sorted(rows))
     (build_dir / "gg_resources_table.inc").write_text(table)
     res_o = build_dir / "gg_resources.o"

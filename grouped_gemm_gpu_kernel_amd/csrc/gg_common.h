@@ -116,16 +116,17 @@ template <> struct VariantTile<GGK_VARIANT_128x64x32> { static constexpr int M =
 template <> struct VariantTile<GGK_VARIANT_64x128x32> { static constexpr int M = 64, N = 128; };
 template <> struct VariantTile<GGK_VARIANT_128x64x32_SMALL> { static constexpr int M = 128, N = 64; };
 template <> struct VariantTile<GGK_VARIANT_64x128x32_SMALL> { static constexpr int M = 64, N = 128; };
+template <> struct VariantTile<GGK_VARIANT_64x64x16_SMALL> { static constexpr int M = 64, N = 64; };
 
 // Kernel shape of (variant, path).  The MFMA path computes a block of TM x TN
 // reference tiles per claim: each A and B value fetched from L2 then feeds TN
 // (A) or TM (B) times the multiply-adds it would feed in a single reference
 // tile, which cuts the L2 -> CU traffic that bounds these kernels, and each
 // wave owns a WAVE_M x WAVE_N block of D, so that every operand fragment it
-// reads from LDS feeds several MFMAs.  128x64x32 (the configuration the
-// reference benchmarks by default): 2 x 4 tiles = 256 x 256 of D, eight waves
-// of 128 x 64.  64x64x16 and 64x128x32: 2 x 2 tiles, waves of 64 x 64.  For
-// launches with few work tiles, 128x64x32 and 64x128x32 also come on 128 x 128
+// reads from LDS feeds several MFMAs.  Every configuration computes 256 x 256
+// of D per claim, eight waves of 128 x 64: 2 x 4 tiles of 128x64x32 (the
+// configuration the reference benchmarks by default), 4 x 4 of 64x64x16, 4 x 2
+// of 64x128x32.  For launches with few work tiles each also comes on 128 x 128
 // work tiles, four waves of 64 x 64 (the _SMALL variants).  The FMA path
 // computes one reference tile with 256 threads.
 template <int V, int PATH> struct KernelShape;
@@ -152,11 +153,16 @@ template <int V, int PATH> struct KernelShape;
 #endif
 
 template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
-  // The GG_* shape macros retune the 128x64x32 variant only.
-  static constexpr bool kTuned = V == GGK_VARIANT_128x64x32;
-  // 128 x 128 work tiles of the small-set variants
-  static constexpr int TM = kTuned ? GG_WORK_TM : (V == GGK_VARIANT_128x64x32_SMALL ? 1 : 2);  // tiles along M
-  static constexpr int TN = kTuned ? GG_WORK_TN : (V == GGK_VARIANT_64x128x32_SMALL ? 1 : 2);  // and along N
+  // The three reference macro-tiles share one work tile, 256 x 256 of D; the
+  // GG_WORK_* macros retune the 128x64x32 variant's, the other GG_* shape
+  // macros all three.
+  static constexpr bool kTuned = V == GGK_VARIANT_128x64x32 || V == GGK_VARIANT_64x64x16 || V == GGK_VARIANT_64x128x32;
+  static constexpr int TM = V == GGK_VARIANT_128x64x32 ? GG_WORK_TM
+                            : kTuned                    ? 256 / VariantTile<V>::M
+                                                        : 128 / VariantTile<V>::M;  // tiles along M
+  static constexpr int TN = V == GGK_VARIANT_128x64x32 ? GG_WORK_TN
+                            : kTuned                    ? 256 / VariantTile<V>::N
+                                                        : 128 / VariantTile<V>::N;  // and along N
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
   static constexpr int WAVE_N = kTuned && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave

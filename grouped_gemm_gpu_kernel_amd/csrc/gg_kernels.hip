@@ -304,7 +304,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       hand_over();
     };
 
-    static_assert(!S::CLASSES || S::TM == 2, "a half of the rows is one row of macro-tiles");
+    static_assert(!S::CLASSES || S::TM % 2 == 0, "a half of the rows is whole rows of macro-tiles");
     int prob, local;
     int half = 0;  // 0: the whole work tile; 1, 2: its first or second half of rows
     if (args.work_table != nullptr) {
@@ -332,7 +332,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
         if (tid < S::TM * S::TN) {
           const int tm = wm * S::TM + tid / S::TN;
           const int tn = wn * S::TN + tid % S::TN;
-          const bool in_half = half == 0 || tid / S::TN == half - 1;
+          const bool in_half = half == 0 || (tid / S::TN) / (S::TM / 2) == half - 1;
           if (in_half && tm < p.tiles_m && tn < p.tiles_n) {
             const int ref = base + tm * p.tiles_n + tn;
             args.tile_map[3 * ref + 0] = prob;
@@ -343,7 +343,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       } else if (half == 0) {
         run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request, after_k_loop);
       } else {
-        // One half of the rows (a whole row of macro-tiles), computed as a
+        // One half of the rows (whole rows of macro-tiles), computed as a
         // problem that ends with that half: its tile has at most BM / 2 rows
         // and runs in a half-height edge class, and each of its D elements is
         // computed as in the whole tile.
@@ -484,12 +484,22 @@ struct KernelSet {
 
 static const KernelSet kKernels[GGK_VARIANT_COUNT][GGK_PATH_COUNT] = {
     GG_ROW(GGK_VARIANT_64x64x16), GG_ROW(GGK_VARIANT_128x64x32), GG_ROW(GGK_VARIANT_64x128x32),
-    GG_ROW(GGK_VARIANT_128x64x32_SMALL), GG_ROW(GGK_VARIANT_64x128x32_SMALL)};
+    GG_ROW(GGK_VARIANT_128x64x32_SMALL), GG_ROW(GGK_VARIANT_64x128x32_SMALL), GG_ROW(GGK_VARIANT_64x64x16_SMALL)};
 #undef GG_ROW
 #undef GG_ENTRY
 
 static bool valid_kernel(int variant, int path) {
   return variant >= 0 && variant < GGK_VARIANT_COUNT && path >= 0 && path < GGK_PATH_COUNT;
+}
+
+// The variant with the same macro-tile on 128 x 128 work tiles, or -1.
+static int small_form(int variant) {
+  switch (variant) {
+    case GGK_VARIANT_64x64x16: return GGK_VARIANT_64x64x16_SMALL;
+    case GGK_VARIANT_128x64x32: return GGK_VARIANT_128x64x32_SMALL;
+    case GGK_VARIANT_64x128x32: return GGK_VARIANT_64x128x32_SMALL;
+    default: return -1;
+  }
 }
 
 static hipError_t fill_launch_shape(int64_t count, dim3* grid) {
@@ -708,8 +718,8 @@ hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc
   if (!valid_kernel(variant, path) || problem == nullptr) return hipErrorInvalidValue;
   // The 64-bit form of the 256 x 256 work tile spills registers: such a
   // problem runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (path == GGK_PATH_MFMA && variant == GGK_VARIANT_128x64x32 && !fits_addr32(kKernels[variant][path], *problem)) {
-    variant = GGK_VARIANT_128x64x32_SMALL;
+  if (path == GGK_PATH_MFMA && small_form(variant) >= 0 && !fits_addr32(kKernels[variant][path], *problem)) {
+    variant = small_form(variant);
   }
   const KernelSet& k = kKernels[variant][path];
   if (problem->tiles_m <= 0 || problem->tiles_n <= 0) return hipSuccess;

@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
 }
 
 // Reference macro-tile of each variant (GGK_VARIANT_*).
-constexpr int kCta[GGK_VARIANT_COUNT][2] = {{64, 64}, {128, 64}, {64, 128}, {128, 64}, {64, 128}};
+constexpr int kCta[GGK_VARIANT_COUNT][2] = {{64, 64}, {128, 64}, {64, 128}, {128, 64}, {64, 128}, {64, 64}};
 
 }  // namespace
 

@@ -51,6 +51,17 @@ int resolve_variant(const KernelConfig& config) {
   return -1;
 }
 
+// The variant with the same macro-tile on 128 x 128 work tiles (the small-set
+// and 64-bit addressing form), or -1.
+int small_variant_of(int variant) {
+  switch (variant) {
+    case GGK_VARIANT_64x64x16: return GGK_VARIANT_64x64x16_SMALL;
+    case GGK_VARIANT_128x64x32: return GGK_VARIANT_128x64x32_SMALL;
+    case GGK_VARIANT_64x128x32: return GGK_VARIANT_64x128x32_SMALL;
+    default: return -1;
+  }
+}
+
 struct RuntimeMode {
   int variant = -1;
   int path = GGK_PATH_FMA;
@@ -702,11 +713,9 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   // A launch with few work tiles is bound by the latency of each tile's
   // stages rather than by bandwidth: when the 128 x 128 work tiles of the
   // small-set variants number at most two per workgroup slot (two
-  // workgroups per CU), 128x64x32 and 64x128x32 run on those instead of their
-  // 256 x 256 / 128 x 256 tiles.  The reference tile map is the same either way.
-  const int small_variant = mode.variant == GGK_VARIANT_128x64x32   ? GGK_VARIANT_128x64x32_SMALL
-                            : mode.variant == GGK_VARIANT_64x128x32 ? GGK_VARIANT_64x128x32_SMALL
-                                                                    : -1;
+  // workgroups per CU), the set runs on those instead of the 256 x 256 ones.
+  // The reference tile map is the same either way.
+  const int small_variant = small_variant_of(mode.variant);
   if (mode.path == GGK_PATH_MFMA && small_variant >= 0) {
     ggk_work_shape small{};
     status = ggk_work_shape_get(small_variant, mode.path, &small);
@@ -741,8 +750,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   }
   // The 64-bit form of the 256 x 256 work tile spills registers: a set that
   // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
-    mode.variant = GGK_VARIANT_128x64x32_SMALL;
+  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && small_variant_of(mode.variant) >= 0) {
+    mode.variant = small_variant_of(mode.variant);
     status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
     if (status != hipSuccess) return status;
     addressing = GGK_ADDR_32;
@@ -1060,8 +1069,8 @@ hipError_t plan_moe(const MoeLayout& layout, const KernelConfig& config, SortMod
   int wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   if (wide < 0) return hipErrorInvalidValue;
   // As in GroupedGemmExecutor::build: no 64-bit 256 x 256 work tiles.
-  if (wide == 1 && mode.path == GGK_PATH_MFMA && mode.variant == GGK_VARIANT_128x64x32) {
-    mode.variant = GGK_VARIANT_128x64x32_SMALL;
+  if (wide == 1 && mode.path == GGK_PATH_MFMA && small_variant_of(mode.variant) >= 0) {
+    mode.variant = small_variant_of(mode.variant);
     status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
     if (status != hipSuccess) return status;
     wide = ggk_needs_addr64(mode.variant, mode.path, &probe);

@@ -45,10 +45,11 @@ typedef struct gg_device_problem_desc {
   int tiles_n;
 } gg_device_problem_desc;
 
-/* Macro-tile shapes (src/grouped_gemm.cu:47-52).  The _SMALL variants have no
- * counterpart in the reference: the same macro-tiles on 128 x 128 work tiles
- * (two workgroups per CU) instead of 256 x 256 (128x64x32) or 128 x 256
- * (64x128x32), which the executor picks for launches with few work tiles (see
+/* Macro-tile shapes (src/grouped_gemm.cu:47-52).  On the MFMA path all three
+ * compute 256 x 256 work tiles (4 x 4, 2 x 4 or 4 x 2 macro-tiles).  The _SMALL
+ * variants have no counterpart in the reference: the same macro-tiles on
+ * 128 x 128 work tiles (two workgroups per CU), which the executor picks for
+ * launches with few work tiles and for sets that need 64-bit addressing (see
  * GroupedGemmExecutor::build). */
 enum {
   GGK_VARIANT_64x64x16 = 0,
@@ -56,7 +57,8 @@ enum {
   GGK_VARIANT_64x128x32 = 2,
   GGK_VARIANT_128x64x32_SMALL = 3,
   GGK_VARIANT_64x128x32_SMALL = 4,
-  GGK_VARIANT_COUNT = 5
+  GGK_VARIANT_64x64x16_SMALL = 5,
+  GGK_VARIANT_COUNT = 6
 };
 
 /* Tile compute path: FMA (the reference's SIMT path) or MFMA (the reference's

@@ -71,7 +71,8 @@ def test_addressing_form_classifier():
 
     for variant, cta_m, cta_n in ((_lib.GGK_VARIANT_64x64x16, 64, 64), (_lib.GGK_VARIANT_128x64x32, 128, 64),
                                   (_lib.GGK_VARIANT_64x128x32, 64, 128), (_lib.GGK_VARIANT_128x64x32_SMALL, 128, 64),
-                                  (_lib.GGK_VARIANT_64x128x32_SMALL, 64, 128)):
+                                  (_lib.GGK_VARIANT_64x128x32_SMALL, 64, 128),
+                                  (_lib.GGK_VARIANT_64x64x16_SMALL, 64, 64)):
         for path in (_lib.GGK_PATH_FMA, _lib.GGK_PATH_MFMA):
             assert lib.ggk_work_shape_get(variant, path, shape) == 0
             assert shape.rows == cta_m * shape.tiles_m and shape.stage_k in (32, 64)
@@ -94,13 +95,18 @@ def test_addressing_form_classifier():
             assert needs(variant, path, 8, 8, ldc=limit_out, c=64, beta=0.5) == 1
             assert needs(variant, path, 8, 8, ldc=limit_out - 1, c=64, beta=0.5) == 0
     assert lib.ggk_needs_addr64(7, 0, _lib.GGDeviceProblemDesc()) == -1
-    assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_128x64x32, _lib.GGK_PATH_MFMA, shape) == 0
-    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 4, 512, 256, 64)
-    # the same macro-tiles on 128 x 128 work tiles, for launches with few work tiles
-    assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_128x64x32_SMALL, _lib.GGK_PATH_MFMA, shape) == 0
-    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (1, 2, 256, 128, 64)
-    assert lib.ggk_work_shape_get(_lib.GGK_VARIANT_64x128x32_SMALL, _lib.GGK_PATH_MFMA, shape) == 0
-    assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == (2, 1, 256, 128, 64)
+    # every configuration on 256 x 256 work tiles, eight waves
+    for variant, want in ((_lib.GGK_VARIANT_128x64x32, (2, 4, 512, 256, 64)),
+                          (_lib.GGK_VARIANT_64x64x16, (4, 4, 512, 256, 64)),
+                          (_lib.GGK_VARIANT_64x128x32, (4, 2, 512, 256, 64)),
+                          # the same macro-tiles on 128 x 128 work tiles, for launches with few work tiles
+                          (_lib.GGK_VARIANT_128x64x32_SMALL, (1, 2, 256, 128, 64)),
+                          (_lib.GGK_VARIANT_64x128x32_SMALL, (2, 1, 256, 128, 64)),
+                          (_lib.GGK_VARIANT_64x64x16_SMALL, (2, 2, 256, 128, 64))):
+        assert lib.ggk_work_shape_get(variant, _lib.GGK_PATH_MFMA, shape) == 0
+        assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == want, variant
+        # the 256 x 256 forms list tail work tiles as row halves
+        assert lib.ggk_work_halves_supported(variant, _lib.GGK_PATH_MFMA) == (1 if want[2] == 512 else 0)
 
 
 def test_failed_build_blocks_run():

@@ -178,7 +178,8 @@ def _variant_of(cfg, shape):
     base = {(64, 64): _lib.GGK_VARIANT_64x64x16, (128, 64): _lib.GGK_VARIANT_128x64x32,
             (64, 128): _lib.GGK_VARIANT_64x128x32}[(cfg.cta_m, cfg.cta_n)]
     small = {_lib.GGK_VARIANT_128x64x32: _lib.GGK_VARIANT_128x64x32_SMALL,
-             _lib.GGK_VARIANT_64x128x32: _lib.GGK_VARIANT_64x128x32_SMALL}.get(base)
+             _lib.GGK_VARIANT_64x128x32: _lib.GGK_VARIANT_64x128x32_SMALL,
+             _lib.GGK_VARIANT_64x64x16: _lib.GGK_VARIANT_64x64x16_SMALL}.get(base)
     for v in (base, small):
         if v is None:
             continue
@@ -258,9 +259,9 @@ def test_grid_size_and_occupancy(torch):
             assert st == 0
             say(f"occupancy {config} mfma={mfma}: {info}")
             assert info.sm_count == 256 and info.using_tensor_cores == mfma
-            # MFMA kernels compute 2 x 2 reference tiles per workgroup with one wave per 64 x 64
-            # block of D; the FMA kernels use 256 threads.
-            want_threads = (2 * cfg.cta_m // 64) * (2 * cfg.cta_n // 64) * 64 if mfma else 256
+            # MFMA kernels compute 256 x 256 of D per workgroup with eight waves of 128 x 64; the FMA
+            # kernels use 256 threads.
+            want_threads = 512 if mfma else 256
             assert info.threads_per_block == want_threads
             assert info.warps_per_block == want_threads // 64 and info.max_warps_per_sm == 32
             assert info.registers_per_thread > 0 and info.active_blocks_per_sm >= 1

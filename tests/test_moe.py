@@ -55,7 +55,7 @@ def test_invalid_layouts_rejected_on_host():
     assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1
     lay.lda = 64
     assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 7, buf, buf, buf, buf, buf, None) == 1  # sort mode
-    assert L.ggk_moe_prepare(5, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1  # variant
+    assert L.ggk_moe_prepare(6, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1  # variant
 
 
 # ---------------------------------------------------------------- GPU

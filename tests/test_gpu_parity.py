@@ -628,13 +628,14 @@ def test_wide_leading_dimensions(torch):
                         f"{config} mfma={mfma} {run} {(m, n, k)}"
 
 
-def test_wide_set_runs_on_128x128_work_tiles(torch):
-    """A 128x64x32 set large enough for 256 x 256 work tiles, plus one problem whose leading dimension
-    needs 64-bit addressing, runs on 128 x 128 work tiles (the 64-bit 256 x 256 form would spill
-    registers): the other problems' D is bit-identical to the same set without the wide problem (256 x
-    256 tiles, 32-bit form), and the wide problem's D is within the oracle bound; the per-problem
-    baseline routes the wide problem the same way."""
-    cfg = KernelConfig.named("128x64x32")
+@pytest.mark.parametrize("config", CONFIGS)
+def test_wide_set_runs_on_128x128_work_tiles(torch, config):
+    """A set large enough for 256 x 256 work tiles, plus one problem whose leading dimension needs
+    64-bit addressing, runs on 128 x 128 work tiles of the same macro-tile (the 64-bit 256 x 256 form
+    would spill registers): the other problems' D is bit-identical to the same set without the wide
+    problem (256 x 256 tiles, 32-bit form), and the wide problem's D is within the oracle bound; the
+    per-problem baseline routes the wide problem the same way."""
+    cfg = KernelConfig.named(config)
     count, m, n, k = 1100, 128, 128, 16
     g = torch.Generator(device="cpu").manual_seed(21)
     a = (torch.rand(m, k, generator=g) * 2 - 1).half().cuda()
@@ -653,7 +654,7 @@ def test_wide_set_runs_on_128x128_work_tiles(torch):
 
     ex = GroupedGemmExecutor()
     assert ex.build(api.prepare_problem_set(fill, cfg, SortMode.kByTiles), cfg) == 0
-    assert ex.schedule()[0].tiles_m == 2  # 256 x 256 work tiles
+    assert (ex.schedule()[0].tiles_m, ex.schedule()[0].tiles_n) == (256 // cfg.cta_m, 256 // cfg.cta_n)
     assert ex.run() == 0
     torch.cuda.synchronize()
     d_large = d.clone()
@@ -663,7 +664,7 @@ def test_wide_set_runs_on_128x128_work_tiles(torch):
     assert ex.build(api.prepare_problem_set(fill + [wide], cfg, SortMode.kByTiles), cfg) == 0
     shape = ex.schedule()[0]
     say(f"wide set: work shape {shape.tiles_m}x{shape.tiles_n}")
-    assert (shape.tiles_m, shape.tiles_n) == (1, 2)  # 128 x 128 work tiles
+    assert (shape.tiles_m, shape.tiles_n) == (128 // cfg.cta_m, 128 // cfg.cta_n)  # 128 x 128 work tiles
     assert ex.run() == 0
     torch.cuda.synchronize()
     assert torch.equal(d, d_large)
@@ -703,7 +704,7 @@ def test_persistent_grid_sizes_and_repeated_runs(torch):
         ex.close()
 
 
-@pytest.mark.parametrize("config", ["128x64x32", "64x128x32"])
+@pytest.mark.parametrize("config", CONFIGS)
 def test_small_set_work_tiles_bit_identical(torch, config):
     """A launch with few work tiles runs on the small-set variant (128 x 128 work tiles, two workgroups
     per CU): 400 problems of 128 x 128 give a grid above one workgroup per CU, which only that variant
@@ -748,7 +749,8 @@ def test_small_set_work_tiles_bit_identical(torch, config):
         assert np.abs(got - want).max() <= tolerance(p.k, 1.0, 1.0, 1.0, p.alpha, p.beta), i
 
 
-def test_edge_class_work_tiles_bit_identical(torch):
+@pytest.mark.parametrize("config", CONFIGS)
+def test_edge_class_work_tiles_bit_identical(torch, config):
     """Work tiles with at most 128 rows and/or 128 columns inside their problem run in the edge
     classes of the 256 x 256 work tile (half-height / half-width stages, more buffers, other wave
     blocks).  A problem that is a row and/or column prefix of a larger one (same A, B and C memory)
@@ -758,7 +760,7 @@ def test_edge_class_work_tiles_bit_identical(torch):
     stage) and several stages deep.  A filler problem keeps the launch on the 256 x 256 kernel
     (grid = one workgroup per CU).  The per-problem baseline must give the same bits, and the
     smallest prefix matches the oracle."""
-    cfg = KernelConfig.named("128x64x32")
+    cfg = KernelConfig.named(config)
     dev = "cuda"
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -769,7 +771,7 @@ def test_edge_class_work_tiles_bit_identical(torch):
     filler_b = torch.rand(16 * 4096, device=dev, generator=g).half()
     filler_d = torch.empty(4096 * 4096, device=dev)
     for k in (64, 333, 1000):
-        say(f"edge classes, K = {k}")
+        say(f"edge classes, {config}, K = {k}")
         a = (torch.rand(full * k, device=dev, generator=g) * 2 - 1).half()
         b = (torch.rand(k * full, device=dev, generator=g) * 2 - 1).half()
         c = torch.rand(full * full, device=dev, generator=g) * 2 - 1

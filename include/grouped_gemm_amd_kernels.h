@@ -83,9 +83,8 @@ enum { GGK_KERNEL_GROUPED = 0, GGK_KERNEL_SINGLE = 1 };
 /* A work-table entry's second int: the work tile's index within its problem
  * in the low bits (GGK_WORK_LOCAL_MASK), and in bits GGK_WORK_HALF_SHIFT and
  * up 0 for the whole work tile or 1 / 2 for its first / second half of rows
- * (one row of macro-tiles each; only for kernels whose work tile is two
- * macro-tiles tall and that have half-height edge classes:
- * ggk_work_halves_supported). */
+ * (128 rows: one or two rows of macro-tiles; only for kernels whose 256-row
+ * work tile has half-height edge classes: ggk_work_halves_supported). */
 #define GGK_WORK_HALF_SHIFT 28
 #define GGK_WORK_LOCAL_MASK ((1 << GGK_WORK_HALF_SHIFT) - 1)
 

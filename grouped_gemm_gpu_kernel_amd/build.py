@@ -137,6 +137,25 @@ def build_library(out_path: Path | None = None, defines: tuple[str, ...] = (), c
     return out
 
 
+def build_host_sanitized(out_path: Path) -> Path:
+    """The library with its host code (grouped_gemm.cpp, c_api.cpp) built by g++ under
+    AddressSanitizer and UndefinedBehaviorSanitizer, linked with the kernel objects of the regular
+    build (build_library first).  Host code only: the GPU code is the regular build's.  A process
+    that loads it needs the sanitizer runtimes preloaded (libasan, libubsan)."""
+    out = Path(out_path)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    objs = []
+    for name in ("grouped_gemm.cpp", "c_api.cpp"):
+        obj = out.parent / (Path(name).stem + "_san.o")
+        _run([*CXX_FLAGS, "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+              f"-I{CSRC_DIR}", "-c", str(CSRC_DIR / name), "-o", str(obj)])
+        objs.append(str(obj))
+    kernel_objs = [str(BUILD / n) for n in ("gg_kernels.o", "gg_moe.o", "gg_resources.o")]
+    _run(["g++", "-shared", "-fsanitize=address,undefined", "-o", str(out), *kernel_objs, *objs,
+          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    return out
+
+
 def build_cpp_tests() -> Path:
     """The C++ drop-in test driver (tests/cpp/test_correctness.cpp), linked
     against the library with an rpath to it."""

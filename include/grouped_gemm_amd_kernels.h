@@ -297,8 +297,8 @@ hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, cons
  * (single_problem_gemm_kernel + launch_single_problem_variant,
  * src/grouped_gemm.cu:677-688, 753-769).  *problem is read on the host and
  * passed by value; a problem with zero tiles launches nothing.  The
- * addressing form is chosen here; a 128x64x32 MFMA problem that needs 64-bit
- * addressing runs on GGK_VARIANT_128x64x32_SMALL's 128 x 128 work tiles
+ * addressing form is chosen here; an MFMA problem that needs 64-bit
+ * addressing runs on the 128 x 128 work tiles of its variant's _SMALL form
  * (same macro-tile, same D). */
 hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,
                              hipStream_t stream);

@@ -156,20 +156,20 @@ template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   // The three reference macro-tiles share one work tile, 256 x 256 of D; the
   // GG_WORK_* macros retune the 128x64x32 variant's, the other GG_* shape
   // macros all three.
-  static constexpr bool kTuned = V == GGK_VARIANT_128x64x32 || V == GGK_VARIANT_64x64x16 || V == GGK_VARIANT_64x128x32;
+  static constexpr bool kLarge = V == GGK_VARIANT_128x64x32 || V == GGK_VARIANT_64x64x16 || V == GGK_VARIANT_64x128x32;
   static constexpr int TM = V == GGK_VARIANT_128x64x32 ? GG_WORK_TM
-                            : kTuned                    ? 256 / VariantTile<V>::M
+                            : kLarge                    ? 256 / VariantTile<V>::M
                                                         : 128 / VariantTile<V>::M;  // tiles along M
   static constexpr int TN = V == GGK_VARIANT_128x64x32 ? GG_WORK_TN
-                            : kTuned                    ? 256 / VariantTile<V>::N
+                            : kLarge                    ? 256 / VariantTile<V>::N
                                                         : 128 / VariantTile<V>::N;  // and along N
   static constexpr int BM = TM * VariantTile<V>::M;
   static constexpr int BN = TN * VariantTile<V>::N;
-  static constexpr int WAVE_N = kTuned && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave
-  static constexpr int WAVE_M = kTuned && GG_WAVE_M < BM ? GG_WAVE_M : 64;                    // rows of D per wave
+  static constexpr int WAVE_N = kLarge && GG_WAVE_N < BN ? GG_WAVE_N : (BN < 64 ? BN : 64);  // columns of D per wave
+  static constexpr int WAVE_M = kLarge && GG_WAVE_M < BM ? GG_WAVE_M : 64;                    // rows of D per wave
   static constexpr int THREADS = (BM / WAVE_M) * (BN / WAVE_N) * kWave;
   // Waves each SIMD must be able to hold (bounds the registers per lane).
-  static constexpr int WAVES_PER_EU = kTuned ? GG_TUNED_WAVES_PER_EU : 2;
+  static constexpr int WAVES_PER_EU = kLarge ? GG_TUNED_WAVES_PER_EU : 2;
   // Stages load straight into LDS.  A 512-thread workgroup has a CU to
   // itself and takes three buffers (two stages in flight) when they fit in
   // LDS, else two; a 256-thread one takes two, so that two of its workgroups
@@ -190,7 +190,7 @@ template <int V> struct KernelShape<V, GGK_PATH_MFMA> {
   // same 512 threads compute it in 64 x 64 (32 x 64) wave blocks; every D
   // element is still one lane's 32x32x16 MFMA chain over ascending k with the
   // same epilogue, so D does not depend on the class.
-  static constexpr bool CLASSES = GG_TILE_CLASSES != 0 && kTuned && BM == 256 && BN == 256 && THREADS == 512;
+  static constexpr bool CLASSES = GG_TILE_CLASSES != 0 && kLarge && BM == 256 && BN == 256 && THREADS == 512;
   using GR = Geometry<BM / 2, BN, GG_STAGE_K, 2, THREADS, 3, true>;       // rows <= BM / 2
   using GC = Geometry<BM, BN / 2, GG_STAGE_K, 2, THREADS, 3, true>;       // columns <= BN / 2
   using GRC = Geometry<BM / 2, BN / 2, GG_STAGE_K, 2, THREADS, 4, true>;  // both

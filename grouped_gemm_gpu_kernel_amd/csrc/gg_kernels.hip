@@ -332,7 +332,8 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
         if (tid < S::TM * S::TN) {
           const int tm = wm * S::TM + tid / S::TN;
           const int tn = wn * S::TN + tid % S::TN;
-          const bool in_half = half == 0 || (tid / S::TN) / (S::TM / 2) == half - 1;
+          constexpr int kHalfRows = S::TM >= 2 ? S::TM / 2 : 1;  // macro-tile rows per half
+          const bool in_half = half == 0 || (tid / S::TN) / kHalfRows == half - 1;
           if (in_half && tm < p.tiles_m && tn < p.tiles_n) {
             const int ref = base + tm * p.tiles_n + tn;
             args.tile_map[3 * ref + 0] = prob;

@@ -1,10 +1,12 @@
 """Grouped FP16 GEMM benchmark on one MI355X.
 
-Headline (the BASELINE metric): grouped TFLOP/s and the fraction of the dense FP16 MFMA peak on the
+Headline: grouped TFLOP/s and the fraction of the dense FP16 MFMA peak on the
 mixed-512 set (512 problems, m, n log-uniform in [64, 1024], k log-uniform in [64, 2048], seed 42,
 macro-tile 128x64x32), for all four sort modes, next to the per-problem-launch baseline, the static
 tail share and the measured tail idle.  A step is one executor.run() over the whole set with every
-operand already resident in HBM.  `value` is the best sort mode's throughput.
+operand already resident in HBM.  `value` is the fastest sort mode's throughput; among modes
+within 1% of the fastest (ties within run-to-run noise) the one with the smallest static tail share
+is reported, with its tail share.
 
 Prints one JSON line.  --gpus above 1 exits: the bench measures one GPU.
 """
@@ -101,6 +103,22 @@ def time_runs(torch, fn, steps: int, warmup: int) -> float:
     stop.synchronize()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+# Sort modes whose times lie within this fraction of the fastest are taken as tied (the spread of
+# repeated runs on one box).
+MODE_TIE = 0.01
+
+
+def headline_mode(rows, times):
+    """(row, ms) of the mode the bench line reports: the fastest, or among the modes within MODE_TIE
+    of it the one with the smallest static tail share (the reference's tail_share,
+    bench/benchmark_grouped_gemm.cu:580-607), so that the reported tail_share is not that of a
+    mode which only won by noise."""
+    fastest = min(times)
+    tied = [(row["tail_share"], ms, i) for i, (row, ms) in enumerate(zip(rows, times)) if ms <= fastest * (1 + MODE_TIE)]
+    _, ms, i = min(tied)
+    return rows[i], ms
 
 
 def warm_clock(torch, fn, seconds: float) -> None:
@@ -556,7 +574,6 @@ def main() -> int:
 
     modes = [SortMode(int(x)) for x in args.modes.split(",")]
     per_mode = []
-    best = None
     # A stream of our own at default priority: the events that time a run are recorded on the stream
     # the kernel is launched on.
     stream = torch.cuda.Stream()
@@ -591,9 +608,8 @@ def main() -> int:
         }
         per_mode.append(row)
         print(f"# {row}", file=sys.stderr, flush=True)
-        if best is None or ms < best[1]:
-            best = (row, ms)
         ex.close()
+    best = headline_mode(per_mode, [ms for ms, _ in timed])
 
     baseline = None
     if not args.no_baseline:

@@ -9,7 +9,7 @@ bench/benchmark_grouped_gemm.cu:464-468) and starts on a 256-byte boundary of
 one pool per operand; odd k or n therefore gives rows that start on 2-byte
 boundaries, which the kernels handle.
 
-Workloads (BASELINE configurations):
+Workloads (the benchmark configurations):
   plumbing16    16 problems, m, n, k uniform in [1, 256]; A, B, C uniform[-1, 1];
                 alpha 1, beta 0.5
   mixed512      512 problems, m, n log-uniform in [64, 1024], k log-uniform in

@@ -110,3 +110,14 @@ def test_committed_traffic_files_parse(bench):
             assert abs(f + w - t) <= 2, f"{path.name} {m}: fetch + write != traffic"
             got = bench.committed_traffic(workload, m)
             assert got is not None and got["bytes"] == pytest.approx(t)
+
+
+def test_headline_mode_breaks_ties_by_tail_share(bench):
+    rows = [{"mode": m, "tail_share": t} for m, t in
+            (("none", 0.078), ("sort_by_k", 0.0185), ("sort_by_tiles", 0.0106), ("sort_by_tiles_then_k", 0.0106))]
+    # all within 1% of the fastest: the smallest static tail share wins, then the faster of equal shares
+    row, ms = bench.headline_mode(rows, [0.2329, 0.2333, 0.2336, 0.2331])
+    assert (row["mode"], ms) == ("sort_by_tiles_then_k", 0.2331)
+    # a clearly faster mode wins whatever its tail share
+    row, ms = bench.headline_mode(rows, [0.2200, 0.2333, 0.2336, 0.2331])
+    assert (row["mode"], ms) == ("none", 0.2200)

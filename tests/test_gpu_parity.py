@@ -3,7 +3,7 @@
 Bars:
   * tile -> (problem, tile_m, tile_n) map, sort permutations, tile offsets and grid size: bit-exact.
   * D: max |D - D_oracle| <= 1e-3 * sqrt(K) * max|A| * max|B| * |alpha| + 1e-6 * (|beta| * max|C| + 1)
-    per problem (the BASELINE bound with |alpha| included, plus a few float32 ulps of the beta*C term).
+    per problem (the target bound with |alpha| included, plus a few float32 ulps of the beta*C term).
   * D is NaN-poisoned before every run, so a tile that is skipped cannot pass on stale output.
   * Full-size sets of every benchmark workload: tests/test_full_size.py.
 """

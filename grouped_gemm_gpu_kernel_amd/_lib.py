@@ -163,6 +163,7 @@ SIGNATURES = {
     "ggk_work_shape_get": (_i, [_i, _i, _P(GGKWorkShape)]),
     "ggk_needs_addr64": (_i, [_i, _i, _P(GGDeviceProblemDesc)]),
     "ggk_work_halves_supported": (_i, [_i, _i]),
+    "ggk_small_variant": (_i, [_i]),
     "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
     "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp,
                                        _vp]),

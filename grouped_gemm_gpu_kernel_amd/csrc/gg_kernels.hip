@@ -493,16 +493,6 @@ static bool valid_kernel(int variant, int path) {
   return variant >= 0 && variant < GGK_VARIANT_COUNT && path >= 0 && path < GGK_PATH_COUNT;
 }
 
-// The variant with the same macro-tile on 128 x 128 work tiles, or -1.
-static int small_form(int variant) {
-  switch (variant) {
-    case GGK_VARIANT_64x64x16: return GGK_VARIANT_64x64x16_SMALL;
-    case GGK_VARIANT_128x64x32: return GGK_VARIANT_128x64x32_SMALL;
-    case GGK_VARIANT_64x128x32: return GGK_VARIANT_64x128x32_SMALL;
-    default: return -1;
-  }
-}
-
 static hipError_t fill_launch_shape(int64_t count, dim3* grid) {
   if (count < 0) return hipErrorInvalidValue;
   int64_t blocks = (count + 255) / 256;
@@ -666,6 +656,15 @@ hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out) {
   return hipSuccess;
 }
 
+int ggk_small_variant(int variant) {
+  switch (variant) {
+    case GGK_VARIANT_64x64x16: return GGK_VARIANT_64x64x16_SMALL;
+    case GGK_VARIANT_128x64x32: return GGK_VARIANT_128x64x32_SMALL;
+    case GGK_VARIANT_64x128x32: return GGK_VARIANT_64x128x32_SMALL;
+    default: return -1;
+  }
+}
+
 int ggk_work_halves_supported(int variant, int path) {
   if (!valid_kernel(variant, path)) return -1;
   return kKernels[variant][path].halves ? 1 : 0;
@@ -719,8 +718,8 @@ hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc
   if (!valid_kernel(variant, path) || problem == nullptr) return hipErrorInvalidValue;
   // The 64-bit form of the 256 x 256 work tile spills registers: such a
   // problem runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (path == GGK_PATH_MFMA && small_form(variant) >= 0 && !fits_addr32(kKernels[variant][path], *problem)) {
-    variant = small_form(variant);
+  if (path == GGK_PATH_MFMA && ggk_small_variant(variant) >= 0 && !fits_addr32(kKernels[variant][path], *problem)) {
+    variant = ggk_small_variant(variant);
   }
   const KernelSet& k = kKernels[variant][path];
   if (problem->tiles_m <= 0 || problem->tiles_n <= 0) return hipSuccess;

@@ -51,17 +51,6 @@ int resolve_variant(const KernelConfig& config) {
   return -1;
 }
 
-// The variant with the same macro-tile on 128 x 128 work tiles (the small-set
-// and 64-bit addressing form), or -1.
-int small_variant_of(int variant) {
-  switch (variant) {
-    case GGK_VARIANT_64x64x16: return GGK_VARIANT_64x64x16_SMALL;
-    case GGK_VARIANT_128x64x32: return GGK_VARIANT_128x64x32_SMALL;
-    case GGK_VARIANT_64x128x32: return GGK_VARIANT_64x128x32_SMALL;
-    default: return -1;
-  }
-}
-
 struct RuntimeMode {
   int variant = -1;
   int path = GGK_PATH_FMA;
@@ -715,7 +704,7 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   // small-set variants number at most two per workgroup slot (two
   // workgroups per CU), the set runs on those instead of the 256 x 256 ones.
   // The reference tile map is the same either way.
-  const int small_variant = small_variant_of(mode.variant);
+  const int small_variant = ggk_small_variant(mode.variant);
   if (mode.path == GGK_PATH_MFMA && small_variant >= 0) {
     ggk_work_shape small{};
     status = ggk_work_shape_get(small_variant, mode.path, &small);
@@ -750,8 +739,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   }
   // The 64-bit form of the 256 x 256 work tile spills registers: a set that
   // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && small_variant_of(mode.variant) >= 0) {
-    mode.variant = small_variant_of(mode.variant);
+  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && ggk_small_variant(mode.variant) >= 0) {
+    mode.variant = ggk_small_variant(mode.variant);
     status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
     if (status != hipSuccess) return status;
     addressing = GGK_ADDR_32;
@@ -1069,8 +1058,8 @@ hipError_t plan_moe(const MoeLayout& layout, const KernelConfig& config, SortMod
   int wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   if (wide < 0) return hipErrorInvalidValue;
   // As in GroupedGemmExecutor::build: no 64-bit 256 x 256 work tiles.
-  if (wide == 1 && mode.path == GGK_PATH_MFMA && small_variant_of(mode.variant) >= 0) {
-    mode.variant = small_variant_of(mode.variant);
+  if (wide == 1 && mode.path == GGK_PATH_MFMA && ggk_small_variant(mode.variant) >= 0) {
+    mode.variant = ggk_small_variant(mode.variant);
     status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
     if (status != hipSuccess) return status;
     wide = ggk_needs_addr64(mode.variant, mode.path, &probe);

@@ -186,6 +186,12 @@ hipError_t ggk_work_shape_get(int variant, int path, ggk_work_shape* out);
  * argument.  No reference counterpart. */
 int ggk_work_halves_supported(int variant, int path);
 
+/* The variant with the same macro-tile on 128 x 128 work tiles (the _SMALL
+ * form, which the executor uses for launches with few work tiles and for sets
+ * that need 64-bit addressing; same D), or -1 when variant has none.  No
+ * reference counterpart. */
+int ggk_small_variant(int variant);
+
 /* Addressing form of a grouped launch.  GGK_ADDR_32: A and B are addressed
  * and C/D with 32-bit offsets from per-tile origins, which needs, for every
  * problem of the launch, 0 <= lda, 0 <= ldb, rows * lda + k + 8 * stage_k <

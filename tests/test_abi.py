@@ -107,6 +107,18 @@ def test_addressing_form_classifier():
         assert (shape.tiles_m, shape.tiles_n, shape.threads, shape.rows, shape.stage_k) == want, variant
         # the 256 x 256 forms list tail work tiles as row halves
         assert lib.ggk_work_halves_supported(variant, _lib.GGK_PATH_MFMA) == (1 if want[2] == 512 else 0)
+    # each large form's 128 x 128 counterpart has the same macro-tile
+    for variant, small in ((_lib.GGK_VARIANT_64x64x16, _lib.GGK_VARIANT_64x64x16_SMALL),
+                           (_lib.GGK_VARIANT_128x64x32, _lib.GGK_VARIANT_128x64x32_SMALL),
+                           (_lib.GGK_VARIANT_64x128x32, _lib.GGK_VARIANT_64x128x32_SMALL)):
+        assert lib.ggk_small_variant(variant) == small
+        big, little = _lib.GGKWorkShape(), _lib.GGKWorkShape()
+        assert lib.ggk_work_shape_get(variant, _lib.GGK_PATH_MFMA, big) == 0
+        assert lib.ggk_work_shape_get(small, _lib.GGK_PATH_MFMA, little) == 0
+        assert big.rows // big.tiles_m == little.rows // little.tiles_m  # macro-tile rows
+    for variant in (_lib.GGK_VARIANT_64x64x16_SMALL, _lib.GGK_VARIANT_128x64x32_SMALL,
+                    _lib.GGK_VARIANT_64x128x32_SMALL, -1, 6):
+        assert lib.ggk_small_variant(variant) == -1
 
 
 def test_failed_build_blocks_run():

@@ -169,6 +169,7 @@ SIGNATURES = {
                                        _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
     "ggk_moe_prepare": (_i, [_i, _i, _P(GGKMoeLayout), _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ggk_moe_layout_check": (_i, [_i, _i, _P(GGKMoeLayout)]),
     "ggk_launch_grouped_device": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp]),
     "ggk_kernel_resources_get": (_i, [_i, _i, _i, _P(GGKKernelResources)]),
     "ggk_occupancy": (_i, [_i, _i, c_int_p]),

@@ -5,7 +5,6 @@ Produces, in-tree:
   grouped_gemm_gpu_kernel_amd/_build/bin/test_correctness   C++ drop-in test driver
   grouped_gemm_gpu_kernel_amd/_build/bin/benchmark_grouped_gemm   benchmark harness (reference CLI)
   grouped_gemm_gpu_kernel_amd/_build/bin/vendor_hipblaslt   hipBLASLt comparison program (bench only)
-  grouped_gemm_gpu_kernel_amd/_build/bin/stream_probe   LDS-DMA streaming probe (measurement aid)
   oracle/liboracle.so                                       CPU oracle (test infrastructure)
 
 Steps: hipcc compiles the kernels for gfx950 with the compiler's resource
@@ -195,16 +194,6 @@ def build_vendor_baseline() -> Path:
     return exe
 
 
-def build_stream_probe() -> Path:
-    """The LDS-DMA streaming probe (bench/stream_probe.hip): a measurement aid, not part of the
-    library."""
-    bin_dir = BUILD / "bin"
-    bin_dir.mkdir(parents=True, exist_ok=True)
-    exe = bin_dir / "stream_probe"
-    _run([HIPCC, *HIP_FLAGS, str(PKG / "bench" / "stream_probe.hip"), "-o", str(exe)])
-    return exe
-
-
 def build_oracle() -> Path:
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
     return ROOT / "oracle" / "liboracle.so"
@@ -218,7 +207,6 @@ def main(argv: list[str]) -> int:
         build_cpp_tests()
     build_bench_driver()
     build_vendor_baseline()
-    build_stream_probe()
     print(f"built {LIB_DIR / LIB_NAME}")
     return 0
 

@@ -551,9 +551,12 @@ hipError_t ggk_event_record_launch(hipEvent_t event, hipStream_t stream, int* re
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   hipError_t st = hipStreamIsCapturing(stream, &capture);
   if (st != hipSuccess) return st;
-  if (capture != hipStreamCaptureStatusNone) return hipSuccess;
+  if (capture != hipStreamCaptureStatusNone) {
+    if (recorded != nullptr) *recorded = GGK_LAUNCH_CAPTURED;
+    return hipSuccess;
+  }
   st = hipEventRecord(event, stream);
-  if (st == hipSuccess && recorded != nullptr) *recorded = 1;
+  if (st == hipSuccess && recorded != nullptr) *recorded = GGK_LAUNCH_RECORDED;
   return st;
 }
 

@@ -456,14 +456,10 @@ extern "C" __attribute__((visibility("hidden"))) hipError_t gg_moe_scratch(void*
   return hipSuccess;
 }
 
-extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts,
-                                      int sort_mode, gg_device_problem_desc* d_problems, int* d_offsets,
-                                      int* d_sorted_to_original, int* d_order, int* d_header, hipStream_t stream) {
-  if (layout == nullptr || variant < 0 || variant >= GGK_VARIANT_COUNT || sort_mode < 0 || sort_mode > 3) {
-    return hipErrorInvalidValue;
-  }
+extern "C" hipError_t ggk_moe_layout_check(int variant, int path, const ggk_moe_layout* layout) {
+  if (layout == nullptr || variant < 0 || variant >= GGK_VARIANT_COUNT) return hipErrorInvalidValue;
   ggk_work_shape work{};
-  hipError_t st = ggk_work_shape_get(variant, path, &work);
+  const hipError_t st = ggk_work_shape_get(variant, path, &work);
   if (st != hipSuccess) return st;
   const ggk_moe_layout& L = *layout;
   const int n1 = L.n > 1 ? L.n : 1;
@@ -478,8 +474,23 @@ extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layou
   const long long row_tiles = (long long)L.max_rows / cta_m + L.experts;
   const long long col_tiles = ((long long)L.n + cta_n - 1) / cta_n;
   if (row_tiles * col_tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (L.a == nullptr || L.b == nullptr || L.d == nullptr || d_counts == nullptr || d_problems == nullptr ||
-      d_offsets == nullptr || d_sorted_to_original == nullptr || d_order == nullptr || d_header == nullptr) {
+  if (L.a == nullptr || L.b == nullptr || L.d == nullptr) return hipErrorInvalidDevicePointer;
+  return hipSuccess;
+}
+
+extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts,
+                                      int sort_mode, gg_device_problem_desc* d_problems, int* d_offsets,
+                                      int* d_sorted_to_original, int* d_order, int* d_header, hipStream_t stream) {
+  if (sort_mode < 0 || sort_mode > 3) return hipErrorInvalidValue;
+  hipError_t st = ggk_moe_layout_check(variant, path, layout);
+  if (st != hipSuccess) return st;
+  ggk_work_shape work{};
+  st = ggk_work_shape_get(variant, path, &work);
+  if (st != hipSuccess) return st;
+  const ggk_moe_layout& L = *layout;
+  const int cta_m = kCta[variant][0], cta_n = kCta[variant][1];
+  if (d_counts == nullptr || d_problems == nullptr || d_offsets == nullptr || d_sorted_to_original == nullptr ||
+      d_order == nullptr || d_header == nullptr) {
     return hipErrorInvalidDevicePointer;
   }
   MoeArgs args{L,         d_counts,  sort_mode,  cta_m, cta_n, work.tiles_m, work.tiles_n, work.stage_k, d_problems,

@@ -364,28 +364,41 @@ Schedule plan_schedule(const std::vector<DeviceProblemDesc>& problems, const std
 // scheduler state, each part starting on a 256-byte boundary (the state's
 // counters then sit on 128-byte lines of their own).  Launches read it until
 // they end, so it is rewritten or freed only after the last launch's event
-// (recorded on that launch's stream) has completed.
+// (recorded on that launch's stream) has completed.  A launch captured into a
+// graph records no event, and the graph may be replayed on any stream at any
+// later time: once a launch was captured, every wait is for the whole device
+// instead, until the allocation is released (the device must then not be
+// capturing).
 struct DeviceBuffer {
   void* base = nullptr;
   size_t capacity = 0;  // bytes
   int device = -1;
   hipEvent_t last_launch = nullptr;
   bool launched = false;  // an event was recorded since the last wait
+  bool captured = false;  // a launch was captured since the allocation was made
 
   static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
   hipError_t wait_launches() {
+    if (captured) {
+      // Replays of the captured launch may be running on any stream; a
+      // device-wide wait also covers the recorded event.
+      launched = false;
+      return ggk_device_synchronize();
+    }
     if (!launched) return hipSuccess;
     launched = false;
     return ggk_event_synchronize(last_launch);
   }
 
-  // Records the event after a launch on `stream` (not while it is captured).
+  // Records the event after a launch on `stream`, or notes that the launch
+  // was captured.
   hipError_t note_launch(hipStream_t stream) {
     if (last_launch == nullptr) return hipSuccess;
     int recorded = 0;
     const hipError_t status = ggk_event_record_launch(last_launch, stream, &recorded);
-    if (recorded) launched = true;
+    if (recorded == GGK_LAUNCH_RECORDED) launched = true;
+    if (recorded == GGK_LAUNCH_CAPTURED) captured = true;
     return status;
   }
 
@@ -426,6 +439,7 @@ struct DeviceBuffer {
     device = -1;
     last_launch = nullptr;
     launched = false;
+    captured = false;
   }
 };
 
@@ -1065,6 +1079,11 @@ hipError_t plan_moe(const MoeLayout& layout, const KernelConfig& config, SortMod
     wide = ggk_needs_addr64(mode.variant, mode.path, &probe);
   }
   plan->addressing = wide == 1 ? GGK_ADDR_64 : GGK_ADDR_32;
+  // The prepare kernel's own layout checks, made here so that a layout it
+  // would reject fails build() and the allocation-free call before anything
+  // is launched.
+  status = ggk_moe_layout_check(mode.variant, mode.path, &L);
+  if (status != hipSuccess) return status;
 
   OccupancyInfo occupancy{};
   status = cached_occupancy(config, mode, &occupancy);

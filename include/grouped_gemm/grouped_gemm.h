@@ -130,8 +130,12 @@ hipError_t query_occupancy(const KernelConfig& config, OccupancyInfo* info);
 // include/grouped_gemm/grouped_gemm.cuh:94-115.  build() uploads the sorted
 // descriptors and tile offsets once; run() launches one persistent grid on the
 // given stream.  Not thread-safe: runs of one executor must not overlap (they
-// share one scheduler state).  Device buffers are released on destruction,
-// move-assignment and rebuild, after a device synchronisation.
+// share one scheduler state).  Device buffers are rewritten or released on
+// rebuild, move-assignment and destruction only after the executor's last
+// launch has completed (an event recorded on that launch's stream); once a
+// run was captured into a graph, after a device synchronisation instead, since
+// the graph's replays may run on any stream (no capture may then be in
+// progress on the device).
 class GroupedGemmExecutor {
  public:
   GroupedGemmExecutor();

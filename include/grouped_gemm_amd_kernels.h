@@ -140,14 +140,18 @@ hipError_t ggk_device_synchronize(void);
 
 /* Completion tracking of an executor's launches (no reference counterpart: the
  * reference frees its buffers with cudaFree, which waits for the whole device).
- * An executor records its event after each launch on the launch's stream --
- * not while that stream is being captured into a graph -- and waits for it
- * before it rewrites or frees the buffers those launches read.  Events are
- * created with timing disabled. */
+ * An executor records its event after each launch on the launch's stream and
+ * waits for it before it rewrites or frees the buffers those launches read.  A
+ * launch captured into a graph has no event (its replays run later, on streams
+ * the executor never sees): the executor then waits for the whole device
+ * instead.  Events are created with timing disabled. */
 hipError_t ggk_event_create(hipEvent_t* event);
 hipError_t ggk_event_destroy(hipEvent_t event);
-/* Records `event` on `stream` unless the stream is capturing; *recorded (may
- * be NULL) tells which. */
+/* Records `event` on `stream` unless the stream is capturing.  *recorded (may
+ * be NULL) tells which: GGK_LAUNCH_RECORDED (1) when the event was recorded,
+ * GGK_LAUNCH_CAPTURED (2) when the stream is capturing, 0 on failure. */
+#define GGK_LAUNCH_RECORDED 1
+#define GGK_LAUNCH_CAPTURED 2
 hipError_t ggk_event_record_launch(hipEvent_t event, hipStream_t stream, int* recorded);
 hipError_t ggk_event_synchronize(hipEvent_t event);
 
@@ -288,6 +292,16 @@ typedef struct ggk_moe_layout {
 hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layout* layout, const int* d_counts, int sort_mode,
                            gg_device_problem_desc* d_problems, int* d_offsets, int* d_sorted_to_original,
                            int* d_order, int* d_header, hipStream_t stream);
+
+/* The host-side checks ggk_moe_prepare makes of a layout before it launches
+ * anything (no reference counterpart: the reference has no device-side
+ * prepare): hipErrorInvalidValue for an expert count outside
+ * [1, GGK_MOE_MAX_EXPERTS], negative n, k or max_rows, lda < k, ldb or ldd
+ * < n, a negative stride_b, ldc < n with C given, or a tile count that could
+ * overflow an int; hipErrorInvalidDevicePointer for a null A, B or D.
+ * MoeGroupedGemm::build and the allocation-free entry point call it before
+ * any launch, so a rejected layout writes nothing. */
+hipError_t ggk_moe_layout_check(int variant, int path, const ggk_moe_layout* layout);
 
 /* The grouped launch of a device-prepared set: the same kernel as
  * ggk_launch_grouped, which reads the work-tile total and the chunk bounds

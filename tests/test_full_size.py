@@ -3,15 +3,24 @@
 4096), the method of the reference's own test (tests/test_correctness.cu:85-102, 216-247): the
 same inputs through every path, then the outputs against the CPU host GEMM.
 
-Bars (size-independent properties at full size, plus sampled elements):
+Bars (size-independent properties at full size, plus checked elements):
   * D is NaN-poisoned before every run; afterwards exactly the padding between the problems' output
     blocks is still NaN (every element of every non-empty problem was written, nothing else was).
   * The four sort modes and the per-problem-launch baseline give bit-identical D (each output tile's
     arithmetic does not depend on the order or the workgroup that computes it); on the MoE shape the
     device-side prepare (MoeGroupedGemm) gives the host-prepared D bit for bit as well.
-  * At least 8 seeded elements of every non-empty problem match the oracle's host GEMM within
-    1e-3 * sqrt(K) * max|A_row| * max|B_col| * |alpha| + 1e-6 * (|beta| * |C| + 1).
+  * Against the oracle's host GEMM, within
+    1e-3 * sqrt(K) * max|A_row| * max|B_col| * |alpha| + 1e-6 * (|beta| * |C| + 1):
+      - 8 seeded elements of every non-empty problem, its corners among them;
+      - one seeded row in every 32-row band of every non-empty problem, all of its columns (problems
+        of at most 2^21 multiply-adds whole): every wave block of every work tile -- 32 x 64 of D at
+        the smallest, in whole 32-row groups -- holds checked elements, in every edge class;
+      - every element of the largest problem of the set (dense64: problem 0 of 64 equal ones;
+        long-tail: 4090 x 3875 x 7430; MoE: the largest expert, 4891 x 14336 x 4096), as the
+        reference's check_outputs compares every element (tests/test_correctness.cu:216-247).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -23,6 +32,9 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 SAMPLES_PER_PROBLEM = 8
+ROW_BAND = 32  # rows per band of the row-band check: the height of the smallest wave block
+WHOLE_MACS = 1 << 21  # problems up to this many multiply-adds are checked whole by the row-band check
+ORACLE_THREADS = max(1, min(16, os.cpu_count() or 1))  # the box's CPU share
 
 
 def say(msg):
@@ -110,6 +122,85 @@ def _check_samples(torch, dw, d_pool, seed, what, rows_of=None):
     say(f"{what}: {idx.size} samples over {probs.size} problems, max error {float(err.max()):.3g}")
 
 
+def _check_rows(torch, dw, d_pool, i, rows, what, rows_of=None):
+    """Rows `rows` of problem i's D, every column, against the oracle's host GEMM (OpenMP form on the
+    host's cores, bit-identical to the literal loop) on the same rows of A and C and all of B.
+    Returns the largest error."""
+    spec = dw.spec
+    m, n, k = int(spec.m[i]), int(spec.n[i]), int(spec.k[i])
+    alpha, beta = float(spec.alpha[i]), float(spec.beta[i])
+    dev = dw.a.device
+    rows = np.asarray(rows, np.int64)
+    r = len(rows)
+    kk = max(k, 1)
+    if k > 0:
+        a_idx = torch.from_numpy(int(dw.a_off[i]) + rows[:, None] * k + np.arange(k)[None, :]).to(dev)
+        a_rows = dw.a[a_idx]
+        b_all = dw.b[int(dw.b_off[i]):int(dw.b_off[i]) + k * n]
+        amax = a_rows.view(torch.float16).float().abs().amax(1).cpu().numpy().astype(np.float64)
+        bmax = b_all.view(torch.float16).view(k, n).float().abs().amax(0).cpu().numpy().astype(np.float64)
+        a_host = a_rows.cpu().numpy().view(np.uint16).reshape(-1)
+        b_host = b_all.cpu().numpy().view(np.uint16)
+    else:
+        amax, bmax = np.zeros(r), np.zeros(n)
+        a_host = np.zeros(1, np.uint16)
+        b_host = np.zeros(1, np.uint16)
+    cols = torch.arange(n, device=dev)
+    c_host = None
+    if dw.has_c:
+        c_idx = torch.from_numpy(int(dw.c_off[i]) + rows * n).to(dev)[:, None] + cols[None, :]
+        c_host = dw.c[c_idx].cpu().numpy().reshape(-1)
+    if rows_of is None:
+        d_start = torch.from_numpy(int(dw.d_off[i]) + rows * n).to(dev)
+    else:
+        d_start = torch.from_numpy(np.array([rows_of(i, int(x)) for x in rows], np.int64)).to(dev)
+    got = d_pool[d_start[:, None] + cols[None, :]].cpu().numpy().astype(np.float64)
+    want = O.gemm(r, n, k, a_host, kk, b_host, n, c_host, n, alpha, beta,
+                  threads=ORACLE_THREADS)[:r * n].reshape(r, n).astype(np.float64)
+    cabs = np.abs(c_host.reshape(r, n)) if c_host is not None else 0.0
+    tol = 1e-3 * np.sqrt(kk) * amax[:, None] * bmax[None, :] * abs(alpha) + 1e-6 * (abs(beta) * cabs + 1.0)
+    err = np.abs(got - want)
+    bad = np.argwhere(~(err <= tol))
+    if bad.size:
+        y, x = bad[0]
+        raise AssertionError(f"{what}: problem {i} ({m}x{n}x{k}): {len(bad)} of {r * n} checked elements outside "
+                             f"the bound, first ({rows[y]}, {x}) got {got[y, x]} want {want[y, x]} tol {tol[y, x]}")
+    return float(err.max()) if err.size else 0.0
+
+
+def _check_row_bands(torch, dw, d_pool, seed, what):
+    """One seeded row in every ROW_BAND-row band of every non-empty problem, all columns (problems of
+    at most WHOLE_MACS multiply-adds whole), against the oracle."""
+    spec = dw.spec
+    rng = np.random.default_rng(seed)
+    live = np.flatnonzero(_live(spec))
+    worst, elements = 0.0, 0
+    for j, i in enumerate(live):
+        m, n, k = int(spec.m[i]), int(spec.n[i]), int(spec.k[i])
+        if m * n * max(k, 1) <= WHOLE_MACS:
+            rows = np.arange(m, dtype=np.int64)
+        else:
+            starts = np.arange(0, m, ROW_BAND, dtype=np.int64)
+            rows = starts + (rng.random(starts.size) * np.minimum(ROW_BAND, m - starts)).astype(np.int64)
+        worst = max(worst, _check_rows(torch, dw, d_pool, int(i), rows, what))
+        elements += len(rows) * n
+        if (j + 1) % 256 == 0:
+            say(f"{what}: row bands of {j + 1} of {live.size} problems checked")
+    say(f"{what}: row bands, {elements} elements over {live.size} problems, max error {worst:.3g}")
+
+
+def _check_whole_problem(torch, dw, d_pool, i, what, rows_of=None):
+    """Every element of problem i against the oracle."""
+    m, n, k = int(dw.spec.m[i]), int(dw.spec.n[i]), int(dw.spec.k[i])
+    say(f"{what}: whole problem {i} ({m}x{n}x{k}) against the oracle on {ORACLE_THREADS} threads")
+    worst = _check_rows(torch, dw, d_pool, int(i), np.arange(m, dtype=np.int64), what, rows_of)
+    say(f"{what}: whole problem {i}: {m * n} elements, max error {worst:.3g}")
+
+
+def _largest_problem(spec) -> int:
+    return int(np.argmax(spec.m.astype(np.int64) * spec.n * np.maximum(spec.k, 1) * _live(spec)))
+
+
 def _run_modes_and_baseline(torch, dw, cfg, what, baseline=True):
     """Runs every sort mode (and the per-problem baseline) on freshly poisoned D; all must give the
     same bits.  Returns the bits of D (a GPU tensor) after the first mode."""
@@ -145,6 +236,9 @@ def test_full_size_workload(torch, name):
     cfg = KernelConfig.named(spec.config)
     _run_modes_and_baseline(torch, dw, cfg, name)
     _check_samples(torch, dw, dw.d, 21, name)
+    _check_row_bands(torch, dw, dw.d, 24, name)
+    if name != "mixed512":
+        _check_whole_problem(torch, dw, dw.d, _largest_problem(spec), name)
     if name == "mixed512":
         # three whole problems against the oracle
         probs = dw.problems()
@@ -170,6 +264,9 @@ def test_full_size_moe64_host_and_device_prepare(torch):
     cfg = KernelConfig.named(spec.config)
     ref = _run_modes_and_baseline(torch, dw, cfg, "moe64 host")
     _check_samples(torch, dw, dw.d, 22, "moe64 host")
+    _check_row_bands(torch, dw, dw.d, 25, "moe64 host")
+    # the largest expert whole; the device-prepared D of every expert equals this D bit for bit (below)
+    _check_whole_problem(torch, dw, dw.d, _largest_problem(spec), "moe64 host")
 
     e, k, n = spec.count, int(spec.k[0]), int(spec.n[0])
     rows = spec.m.astype(np.int64)

@@ -704,6 +704,50 @@ def test_persistent_grid_sizes_and_repeated_runs(torch):
         ex.close()
 
 
+def test_rebuild_after_captured_run_waits_for_replays(torch):
+    """run() captured into a graph, replayed, and the executor rebuilt at once (no host wait): the
+    rebuild rewrites the executor's device buffer, which the replay is still reading, only after the
+    device is idle, so the replay's D and the rebuilt executor's D both equal eager runs."""
+    cfg = KernelConfig.named("128x64x32")
+    first = DeviceWorkload(make_spec("mixed512"))
+    second = DeviceWorkload(make_spec("plumbing16"))
+    prep1 = api.prepare_problem_set(first.problems(), cfg, SortMode.kByTiles)
+    prep2 = api.prepare_problem_set(second.problems(), cfg, SortMode.kByK)
+    ex = GroupedGemmExecutor()
+    assert ex.build(prep1, cfg) == 0
+    first.poison_d()
+    assert ex.run() == 0
+    torch.cuda.synchronize()
+    want1 = first.d.cpu().numpy().view(np.uint32).copy()
+    ex2 = GroupedGemmExecutor()
+    assert ex2.build(prep2, cfg) == 0
+    second.poison_d()
+    assert ex2.run() == 0
+    torch.cuda.synchronize()
+    want2 = second.d.cpu().numpy().view(np.uint32).copy()
+    ex2.close()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert ex.run(torch.cuda.current_stream()) == 0
+    side = torch.cuda.Stream()
+    for rep in range(3):
+        say(f"captured run, replay {rep}, then rebuild without a host wait")
+        first.poison_d()
+        assert ex.build(prep1, cfg) == 0  # back to the captured set (same buffer, same contents)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):  # a non-blocking stream: the host copies do not order after it
+            graph.replay()
+        # the replay is in flight: this rebuild must wait for it before rewriting the buffer
+        assert ex.build(prep2, cfg) == 0
+        second.poison_d()
+        assert ex.run() == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(first.d.cpu().numpy().view(np.uint32), want1), rep
+        assert np.array_equal(second.d.cpu().numpy().view(np.uint32), want2), rep
+    ex.close()
+    del graph
+
+
 @pytest.mark.parametrize("config", CONFIGS)
 def test_small_set_work_tiles_bit_identical(torch, config):
     """A launch with few work tiles runs on the small-set variant (128 x 128 work tiles, two workgroups

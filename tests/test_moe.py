@@ -56,6 +56,15 @@ def test_invalid_layouts_rejected_on_host():
     lay.lda = 64
     assert L.ggk_moe_prepare(1, 1, ctypes.byref(lay), buf, 7, buf, buf, buf, buf, buf, None) == 1  # sort mode
     assert L.ggk_moe_prepare(6, 1, ctypes.byref(lay), buf, 2, buf, buf, buf, buf, buf, None) == 1  # variant
+    # the same checks on their own, as build() and the allocation-free call make them before any launch
+    assert L.ggk_moe_layout_check(1, 1, ctypes.byref(lay)) == 0
+    for field, bad in (("lda", 10), ("max_rows", -1), ("ldb", 63), ("ldd", 0), ("stride_b", -1), ("experts", 0)):
+        good = getattr(lay, field)
+        setattr(lay, field, bad)
+        assert L.ggk_moe_layout_check(1, 1, ctypes.byref(lay)) == 1, field
+        setattr(lay, field, good)
+    lay.b = None
+    assert L.ggk_moe_layout_check(1, 1, ctypes.byref(lay)) == _lib.HIP_ERROR_INVALID_DEVICE_POINTER
 
 
 # ---------------------------------------------------------------- GPU

@@ -52,6 +52,8 @@ def parse_args():
                     help="only run a plain device-to-device copy of MIB MiB a few times (for scaling HBM "
                          "byte counters of a profiler run) and exit")
     ap.add_argument("--no-moe-device", action="store_true", help="skip the device-side MoE prepare timing")
+    ap.add_argument("--phases", action="store_true",
+                    help="also report per-work-tile phase cycles of each mode (traced launches with phase stamps)")
     ap.add_argument("--profile-summary", nargs="+", metavar="DIR",
                     help="only summarize rocprofv3 CSV output folders (kernel trace and/or counters) and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -176,6 +178,83 @@ def measured_tail_idle(torch, ex, runs: int = 3) -> float:
         t0, t1 = c[:, 0].min(), c[:, 1].max()
         shares.append(float(((t1 - c[:, 1]).sum()) / (grid * (t1 - t0))) if t1 > t0 else 0.0)
     return statistics.median(shares)
+
+
+def tile_phases(torch, ex, runs: int = 3) -> dict:
+    """Where a work tile's time goes, from the phase stamps of traced launches (core-clock cycles,
+    s_memtime; GGK_PHASE_* in include/grouped_gemm_amd_kernels.h).  Per class of work tile (by its
+    rows and columns inside the problem against half the work tile, and the row halves of the
+    work table): the mean cycles from its start until one wave's first-stage loads have landed
+    (first_stage), until every wave has them (k_loop_start), the k-loop per k-stage (summed cycles
+    over summed stages), the hand-over of the next index, the epilogue until its last wave is done,
+    and next_start: from the last epilogue wave's end to the same workgroup's next tile start
+    (negative where its first waves start the next tile while the slowest still stores).  The
+    median launch of `runs`."""
+    import numpy as np
+
+    from grouped_gemm_gpu_kernel_amd import _lib
+
+    n = ex.launched_work_tiles()
+    P = _lib.GGK_PHASE_COUNT
+    buf = torch.zeros(P * max(1, n), dtype=torch.int64, device="cuda")
+    launches = []
+    for _ in range(runs):
+        buf.zero_()
+        st = ex.run_traced(0, 0, None, buf.data_ptr())
+        if st != 0:
+            raise RuntimeError(f"traced run hipError_t {st}")
+        torch.cuda.synchronize()
+        ph = buf.cpu().numpy().reshape(-1, P)[:n]
+        ph = ph[ph[:, _lib.GGK_PHASE_START] > 0]
+        launches.append((float(ph[:, _lib.GGK_PHASE_EPILOGUE_END].max() - ph[:, _lib.GGK_PHASE_START].min()), ph))
+    launches.sort(key=lambda x: x[0])
+    ph = launches[len(launches) // 2][1]
+    who = ph[:, _lib.GGK_PHASE_WHO]
+    wg = who & 0xFFFFF
+    half = (who >> 20) & 3
+    rows = (who >> 22) & 0xFFF
+    cols = (who >> 34) & 0xFFF
+    stages = (who >> 46) & 0x1FFFF
+    start, first = ph[:, _lib.GGK_PHASE_START], ph[:, _lib.GGK_PHASE_FIRST_STAGE]
+    kl, ke = ph[:, _lib.GGK_PHASE_K_LOOP], ph[:, _lib.GGK_PHASE_K_END]
+    epi, epi_end = ph[:, _lib.GGK_PHASE_EPILOGUE], ph[:, _lib.GGK_PHASE_EPILOGUE_END]
+    # gap: from a tile's last epilogue wave to the same workgroup's next tile start (core clocks of
+    # one workgroup's CU, ordered by the wall clock)
+    gap = np.full(len(ph), np.nan)
+    order = np.lexsort((ph[:, _lib.GGK_PHASE_WALL], wg))
+    same = wg[order][1:] == wg[order][:-1]
+    gap[order[:-1][same]] = start[order[1:][same]] - epi_end[order[:-1][same]]
+    bm = int(rows.max()) if len(rows) else 0
+    bn = int(cols.max()) if len(cols) else 0
+    classes = {
+        "whole": (half == 0) & (rows > bm // 2) & (cols > bn // 2),
+        "rows_le_half": (half == 0) & (rows <= bm // 2) & (cols > bn // 2),
+        "cols_le_half": (half == 0) & (rows > bm // 2) & (cols <= bn // 2),
+        "both_le_half": (half == 0) & (rows <= bm // 2) & (cols <= bn // 2),
+        "row_halves": half > 0,
+        "all": np.ones(len(ph), bool),
+    }
+    out = {"work_tiles": int(len(ph)), "work_tile_rows": bm, "work_tile_cols": bn}
+    for name, sel in classes.items():
+        if not sel.any():
+            continue
+        g = gap[sel]
+        g = g[~np.isnan(g)]
+        out[name] = {
+            "tiles": int(sel.sum()), "stages": round(float(stages[sel].mean()), 2),
+            "first_stage": round(float((first - start)[sel].mean())),
+            "k_loop_start": round(float((kl - start)[sel].mean())),
+            "k_loop_per_stage": round(float((ke - kl)[sel].sum() / max(1, stages[sel].sum()))),
+            "hand_over": round(float((epi - ke)[sel].mean())),
+            "epilogue": round(float((epi_end - epi)[sel].mean())),
+            "next_start": round(float(g.mean())) if g.size else None,
+        }
+    tile = (epi_end - start).sum()
+    out["share"] = {"to_k_loop": round(float((kl - start).sum() / tile), 4),
+                    "k_loop": round(float((ke - kl).sum() / tile), 4),
+                    "hand_over": round(float((epi - ke).sum() / tile), 4),
+                    "epilogue": round(float((epi_end - epi).sum() / tile), 4)}
+    return out
 
 
 def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int, warm_seconds: float) -> dict:
@@ -598,18 +677,21 @@ def main() -> int:
         ms = time_runs(torch, lambda: ex.run(stream), args.steps, args.warmup)
         # The traced runs right after a mode's timed runs also mark, in a profiler's dispatch list,
         # where that mode's runs end (--profile-summary / --traffic-summary --modes-of-segments).
-        timed.append((ms, measured_tail_idle(torch, ex)))
-    for (mode, prep, ex, prep_ms), (ms, tail_idle) in zip(built, timed):
+        timed.append((ms, measured_tail_idle(torch, ex), tile_phases(torch, ex) if args.phases else None))
+    for (mode, prep, ex, prep_ms), (ms, tail_idle, phases) in zip(built, timed):
         row = {
             "mode": api.sort_mode_name(mode), "prep_ms": round(prep_ms, 3), "kernel_ms": round(ms, 4),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "tiles": prep.total_tiles,
             "grid_ctas": ex.grid_ctas(), "launches": 1,
             "tail_share": round(api.tail_work_share(prep, cfg), 4), "tail_idle_measured": round(tail_idle, 4),
         }
+        if phases is not None:
+            row["tile_phases"] = phases
+            print(f"# tile phases {row['mode']}: {json.dumps(phases)}", file=sys.stderr, flush=True)
         per_mode.append(row)
         print(f"# {row}", file=sys.stderr, flush=True)
         ex.close()
-    best = headline_mode(per_mode, [ms for ms, _ in timed])
+    best = headline_mode(per_mode, [ms for ms, _, _ in timed])
 
     baseline = None
     if not args.no_baseline:

@@ -34,6 +34,9 @@ GGK_ADDR_64 = 1
 GGK_SCHEDULER_CHUNKS = 8
 GGK_SCHEDULER_COUNTER_STRIDE = 32
 GGK_SCHEDULER_STATE_INTS = GGK_SCHEDULER_COUNTER_STRIDE * (GGK_SCHEDULER_CHUNKS + 1)
+GGK_PHASE_WALL, GGK_PHASE_START, GGK_PHASE_FIRST_STAGE, GGK_PHASE_K_LOOP = 0, 1, 2, 3
+GGK_PHASE_K_END, GGK_PHASE_EPILOGUE, GGK_PHASE_EPILOGUE_END, GGK_PHASE_WHO = 4, 5, 6, 7
+GGK_PHASE_COUNT = 8
 GGK_MOE_MAX_EXPERTS = 1024
 GGK_MOE_HEADER_INTS = 16
 GGK_MOE_STATUS = 12
@@ -130,7 +133,8 @@ SIGNATURES = {
     "gg_executor_destroy": (None, [_vp]),
     "gg_executor_build": (_i, [_vp, _P(GGProblemDesc), _i, c_int_p, _i, _i, _P(GGKernelConfig)]),
     "gg_executor_run": (_i, [_vp, _vp]),
-    "gg_executor_run_traced": (_i, [_vp, _vp, _vp, _vp]),
+    "gg_executor_run_traced": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "gg_executor_launched_work_tiles": (_i, [_vp]),
     "gg_executor_problem_count": (_i, [_vp]),
     "gg_executor_total_tiles": (_i, [_vp]),
     "gg_executor_grid_ctas": (_i, [_vp]),
@@ -166,7 +170,7 @@ SIGNATURES = {
     "ggk_small_variant": (_i, [_i]),
     "ggk_launch_grouped": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp]),
     "ggk_launch_grouped_traced": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, c_int_p, _i, _vp, _vp,
-                                       _vp]),
+                                       _vp, _vp]),
     "ggk_launch_single": (_i, [_i, _i, _P(GGDeviceProblemDesc), _vp]),
     "ggk_moe_prepare": (_i, [_i, _i, _P(GGKMoeLayout), _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ggk_moe_layout_check": (_i, [_i, _i, _P(GGKMoeLayout)]),

@@ -206,12 +206,18 @@ class GroupedGemmExecutor:
     def run(self, stream=None) -> int:
         return _lib.lib().gg_executor_run(self._handle, _stream_handle(stream))
 
-    def run_traced(self, tile_map_ptr: int = 0, wg_clock_ptr: int = 0, stream=None) -> int:
+    def run_traced(self, tile_map_ptr: int = 0, wg_clock_ptr: int = 0, stream=None, tile_phases_ptr: int = 0) -> int:
         """Scheduler with instrumentation: tile_map_ptr (device int[3*total_tiles]) receives
         (problem, tile_m, tile_n) per tile instead of computing; wg_clock_ptr (device
-        int64[2*grid]) receives each workgroup's start/end wall clock (100 MHz)."""
+        int64[2*grid]) receives each workgroup's start/end wall clock (100 MHz);
+        tile_phases_ptr (device int64[GGK_PHASE_COUNT * launched_work_tiles()], zeroed) receives
+        each work tile's phase stamps (GGK_PHASE_*)."""
         return _lib.lib().gg_executor_run_traced(self._handle, tile_map_ptr or None, wg_clock_ptr or None,
-                                                 _stream_handle(stream))
+                                                 tile_phases_ptr or None, _stream_handle(stream))
+
+    def launched_work_tiles(self) -> int:
+        """Work-tile indices one launch claims (row halves of the work table counted one each)."""
+        return _lib.lib().gg_executor_launched_work_tiles(self._handle)
 
     def problem_count(self) -> int:
         return _lib.lib().gg_executor_problem_count(self._handle)

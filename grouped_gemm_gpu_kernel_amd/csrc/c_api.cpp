@@ -216,9 +216,13 @@ int gg_executor_run(const gg_executor* executor, hipStream_t stream) {
 }
 
 int gg_executor_run_traced(const gg_executor* executor, int* d_tile_map, long long* d_wg_clock,
-                           hipStream_t stream) {
+                           long long* d_tile_phases, hipStream_t stream) {
   if (executor == nullptr) return hipErrorInvalidDevicePointer;
-  return executor->executor.run_traced(d_tile_map, d_wg_clock, stream);
+  return executor->executor.run_traced(d_tile_map, d_wg_clock, stream, d_tile_phases);
+}
+
+int gg_executor_launched_work_tiles(const gg_executor* executor) {
+  return executor != nullptr ? executor->executor.launched_work_tiles() : 0;
 }
 
 int gg_executor_problem_count(const gg_executor* executor) {

@@ -204,6 +204,31 @@ template <int V> struct KernelShape<V, GGK_PATH_FMA> {
   static constexpr bool CLASSES = false;
 };
 
+// Per-work-tile phase stamps of a traced launch: 8 int64 per work-tile index
+// (GGK_PHASE_* in grouped_gemm_amd_kernels.h).  Core-clock stamps are
+// s_memtime; one wave's record stands for the workgroup except the epilogue
+// end, the latest over the waves.  NoStamps, the untraced kernels' type,
+// compiles to nothing.
+struct NoStamps {
+  __device__ __forceinline__ void mark(int) const {}
+  __device__ __forceinline__ void wave_done() const {}
+};
+struct PhaseStamps {
+  long long* slot;  // this work tile's 8 entries, or null
+  __device__ __forceinline__ void mark(int i) const {
+    if (slot != nullptr && __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) == 0) {
+      slot[i] = static_cast<long long>(__builtin_amdgcn_s_memtime());
+    }
+  }
+  // Every wave, when its epilogue has been issued.
+  __device__ __forceinline__ void wave_done() const {
+    if (slot != nullptr && (threadIdx.x & (kWave - 1)) == 0) {
+      atomicMax(reinterpret_cast<unsigned long long*>(slot + GGK_PHASE_EPILOGUE_END),
+                static_cast<unsigned long long>(__builtin_amdgcn_s_memtime()));
+    }
+  }
+};
+
 // threadIdx.x behind an empty asm: the compiler must assume it changes at
 // every call, so values derived from it are recomputed where they are used
 // instead of being held in registers for the whole persistent kernel.

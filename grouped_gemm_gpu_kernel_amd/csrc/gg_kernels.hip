@@ -63,6 +63,7 @@ struct GroupedArgs {
   int* state;          // chunk c's claim counter at [c * kStride], retired workgroups at [kChunks * kStride]
   int* tile_map;       // traced launches only
   long long* wg_clock; // traced launches only
+  long long* tile_phases;  // traced launches only: GGK_PHASE_COUNT per work-tile index
   int bounds[kChunks + 1];  // chunk c owns work-tile indices [bounds[c], bounds[c + 1])
   // When set, the total and the bounds are read from this device header
   // (written by a device-side prepare in stream order) instead of the two
@@ -209,6 +210,22 @@ __device__ __forceinline__ void work_tile_position(int local, int wtm, int wtn, 
   wm = first + (within - wn * rows);
 }
 
+// The start stamps of a traced work tile: wall clock, core clock, and what it
+// is (workgroup, row half, rows and columns inside the problem, k-stages).
+template <class G>
+__device__ __forceinline__ void mark_tile_start(const PhaseStamps& stamps, int half, const gg_device_problem_desc& p,
+                                                int m0, int n0) {
+  if (stamps.slot != nullptr && __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) == 0) {
+    const long long rows = p.m - m0 < G::BM ? p.m - m0 : G::BM;
+    const long long cols = p.n - n0 < G::BN ? p.n - n0 : G::BN;
+    const long long stages = (p.k + G::BK - 1) / G::BK;
+    stamps.slot[GGK_PHASE_WALL] = wall_clock64();
+    stamps.slot[GGK_PHASE_WHO] =
+        (long long)blockIdx.x | ((long long)half << 20) | (rows << 22) | (cols << 34) | (stages << 46);
+  }
+  stamps.mark(GGK_PHASE_START);
+}
+
 // At least KernelShape::WAVES_PER_EU waves per SIMD: 2 allows 256 VGPRs +
 // AGPRs per lane (a 512-thread workgroup, or two 256-thread ones), 1 allows 512.
 #define GG_KERNEL_ATTRS(V, PATH)                          \
@@ -299,9 +316,14 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       next_t = __builtin_amdgcn_readfirstlane(s_claim[parity]);
       handed = true;
     };
+    // Phase stamps of this work tile (traced launches with a phase buffer only).
+    PhaseStamps stamps{TRACED && args.tile_phases != nullptr ? args.tile_phases + (long long)GGK_PHASE_COUNT * t
+                                                             : nullptr};
     auto after_k_loop = [&]() {
+      stamps.mark(GGK_PHASE_K_END);
       if (!asked) request();
       hand_over();
+      stamps.mark(GGK_PHASE_EPILOGUE);
     };
 
     static_assert(!S::CLASSES || S::TM % 2 == 0, "a half of the rows is whole rows of macro-tiles");
@@ -342,7 +364,12 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
           }
         }
       } else if (half == 0) {
-        run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request, after_k_loop);
+        if constexpr (TRACED) {
+          mark_tile_start<G>(stamps, 0, p, wm * G::BM, wn * G::BN);
+          run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request, after_k_loop, stamps);
+        } else {
+          run_work_tile<S, PATH, WIDE>(p, wm * G::BM, wn * G::BN, lds, request, after_k_loop);
+        }
       } else {
         // One half of the rows (whole rows of macro-tiles), computed as a
         // problem that ends with that half: its tile has at most BM / 2 rows
@@ -352,7 +379,12 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
         const int m0 = wm * G::BM + (half - 1) * (G::BM / 2);
         const int end = m0 + G::BM / 2;
         q.m = end < p.m ? end : p.m;
-        run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request, after_k_loop);
+        if constexpr (TRACED) {
+          mark_tile_start<G>(stamps, half, q, m0, wn * G::BN);
+          run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request, after_k_loop, stamps);
+        } else {
+          run_work_tile<S, PATH, WIDE>(q, m0, wn * G::BN, lds, request, after_k_loop);
+        }
       }
     }
     if (!asked) request();
@@ -613,7 +645,8 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
                                  const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
                                  const int* d_work_offsets, const int* d_order, const int* d_work_table,
                                  int problem_count, int total_work, int* d_state, const int* chunk_bounds, int grid,
-                                 int* d_tile_map, long long* d_wg_clock, hipStream_t stream) {
+                                 int* d_tile_map, long long* d_wg_clock, long long* d_tile_phases,
+                                 hipStream_t stream) {
   if (!valid_kernel(variant, path) || grid <= 0 || problem_count < 0 || total_work < 0 ||
       (addressing != GGK_ADDR_32 && addressing != GGK_ADDR_64)) {
     return hipErrorInvalidValue;
@@ -624,8 +657,9 @@ static hipError_t launch_grouped(int variant, int path, int addressing, bool tra
   }
   if (traced && d_tile_map != nullptr && d_tile_offsets == nullptr) return hipErrorInvalidDevicePointer;
   if (!bounds_valid(chunk_bounds, total_work)) return hipErrorInvalidValue;
-  GroupedArgs args{d_problems, d_tile_offsets, d_work_offsets, d_order, d_work_table, problem_count, total_work,
-                   d_state, traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr, {}, nullptr};
+  GroupedArgs args{d_problems,  d_tile_offsets, d_work_offsets, d_order, d_work_table, problem_count, total_work,
+                   d_state,     traced ? d_tile_map : nullptr, traced ? d_wg_clock : nullptr,
+                   traced ? d_tile_phases : nullptr, {}, nullptr};
   fill_bounds(args, chunk_bounds);
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];
@@ -684,7 +718,7 @@ hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_de
                               int problem_count, int total_work, int* d_state, const int* chunk_bounds, int grid,
                               hipStream_t stream) {
   return launch_grouped(variant, path, addressing, false, d_problems, nullptr, d_work_offsets, d_order, d_work_table,
-                        problem_count, total_work, d_state, chunk_bounds, grid, nullptr, nullptr, stream);
+                        problem_count, total_work, d_state, chunk_bounds, grid, nullptr, nullptr, nullptr, stream);
 }
 
 hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, const gg_device_problem_desc* d_problems,
@@ -699,7 +733,7 @@ hipError_t ggk_launch_grouped_device(int variant, int path, int addressing, cons
     return hipErrorInvalidDevicePointer;
   }
   GroupedArgs args{d_problems, nullptr, d_work_offsets, d_order, nullptr, problem_count, 0, d_state, nullptr, nullptr,
-                   {}, d_header};
+                   nullptr, {}, d_header};
   void* params[] = {&args};
   const KernelSet& k = kKernels[variant][path];
   return hipLaunchKernel(reinterpret_cast<const void*>(k.grouped[addressing]), dim3(grid), dim3(k.threads), params,
@@ -710,10 +744,11 @@ hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
                                      const int* d_work_offsets, const int* d_order, const int* d_work_table,
                                      int problem_count, int total_work, int* d_state, const int* chunk_bounds,
-                                     int grid, int* d_tile_map, long long* d_wg_clock, hipStream_t stream) {
+                                     int grid, int* d_tile_map, long long* d_wg_clock, long long* d_tile_phases,
+                                     hipStream_t stream) {
   return launch_grouped(variant, path, addressing, true, d_problems, d_tile_offsets, d_work_offsets, d_order,
                         d_work_table, problem_count, total_work, d_state, chunk_bounds, grid, d_tile_map, d_wg_clock,
-                        stream);
+                        d_tile_phases, stream);
 }
 
 hipError_t ggk_launch_single(int variant, int path, const gg_device_problem_desc* problem,

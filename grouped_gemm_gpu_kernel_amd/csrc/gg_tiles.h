@@ -30,9 +30,9 @@ namespace gg {
 // runs whole groups of DEPTH steps with no branch; the last steps of a tile
 // are guarded.  The body is unrolled DEPTH times so that every register set
 // is addressed statically.
-template <class G, bool WIDE, class Compute, class OnStart>
+template <class G, bool WIDE, class Compute, class OnStart, class Stamps>
 __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                           Compute&& compute, OnStart&& on_start) {
+                                           Compute&& compute, OnStart&& on_start, const Stamps& stamps) {
   constexpr int D = G::DEPTH;
   const int nk = (p.k + G::BK - 1) / G::BK;
   if (nk <= 0) {
@@ -45,7 +45,9 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
   for (int s = 0; s < D - 1; ++s) loader.issue(s, ring[s]);
   on_start();  // the compiler's waits count the request like any other load
   loader.store(ring[0], 0, lds, 0);
+  stamps.mark(GGK_PHASE_FIRST_STAGE);
   __syncthreads();
+  stamps.mark(GGK_PHASE_K_LOOP);
   auto step = [&](int k, int u) {
     loader.issue(k + D - 1, ring[(u + D - 1) % D]);
     compute(lds + (k & 1) * G::STAGE);
@@ -77,9 +79,9 @@ __device__ __forceinline__ void run_k_loop(const gg_device_problem_desc& p, int 
 // lets it stay in flight (loads complete in order, so one more outstanding
 // operation is exactly that request).  The second step's wait retires it, so
 // it has two stage computations to come back.
-template <class G, class Compute, class OnStart>
+template <class G, class Compute, class OnStart, class Stamps>
 __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                               Compute&& compute, OnStart&& on_start) {
+                                               Compute&& compute, OnStart&& on_start, const Stamps& stamps) {
   constexpr int NBUF = G::BUFFERS;
   constexpr int L = NBUF - 1;
   constexpr int PENDING = (L - 1) * DmaLoader<G>::LOADS;  // loads of later stages allowed in flight
@@ -92,8 +94,10 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
 #pragma unroll
   for (int s = 0; s < L; ++s) loader.issue(s, lds + s * G::STAGE);
   wait_vmcnt<PENDING>();
+  stamps.mark(GGK_PHASE_FIRST_STAGE);
   if (loader.last_stage == 0) loader.fix_last_stage(0, lds);
   stage_barrier();
+  stamps.mark(GGK_PHASE_K_LOOP);
   // One step per iteration, not unrolled: no register set has to be indexed
   // statically, and one copy of the step keeps the code a launch has to fetch
   // into a cold instruction cache small.  u is the buffer of stage k.
@@ -218,9 +222,9 @@ struct MfmaTile {
   // Computes the work tile at (m0, n0); on_start as in the k-loops, and
   // after_k_loop() once by every thread when the k-loop is over (no LDS read
   // of this tile follows it: the epilogue works from registers).
-  template <bool WIDE, class OnStart, class AfterKLoop>
+  template <bool WIDE, class OnStart, class AfterKLoop, class Stamps>
   __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                             OnStart&& on_start, AfterKLoop&& after_k_loop) {
+                                             OnStart&& on_start, AfterKLoop&& after_k_loop, const Stamps& stamps) {
     const int tid = opaque_tid();
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -242,14 +246,14 @@ struct MfmaTile {
       if (live) compute_stage(stage, lane, wm, wn, acc);
     };
     if constexpr (WIDE) {
-      run_k_loop<G, WIDE>(p, m0, n0, lds, compute, on_start);
+      run_k_loop<G, WIDE>(p, m0, n0, lds, compute, on_start, stamps);
     } else {
-      run_k_loop_dma<G>(p, m0, n0, lds, compute, on_start);
+      run_k_loop_dma<G>(p, m0, n0, lds, compute, on_start, stamps);
     }
     after_k_loop();
 
-    if (!live) return;
-    store_tile<WIDE>(p, m0 + wm * WM, n0 + wn * WN, lane, acc);
+    if (live) store_tile<WIDE>(p, m0 + wm * WM, n0 + wn * WN, lane, acc);
+    stamps.wave_done();
   }
 
   // 4 x 4 transpose across the 4 lanes of a quad: lane q holds x[k] = M[q][k]
@@ -549,9 +553,9 @@ struct FmaTile {
 
   // Computes the work tile at (m0, n0); on_start and after_k_loop as in
   // MfmaTile::run.
-  template <bool WIDE, class OnStart, class AfterKLoop>
+  template <bool WIDE, class OnStart, class AfterKLoop, class Stamps>
   __device__ __forceinline__ static void run(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                             OnStart&& on_start, AfterKLoop&& after_k_loop) {
+                                             OnStart&& on_start, AfterKLoop&& after_k_loop, const Stamps& stamps) {
     const int tid = threadIdx.x;
     const int tm = tid >> 4;
     const int tn = tid & 15;
@@ -568,10 +572,13 @@ struct FmaTile {
     run_k_loop<G, WIDE>(p, m0, n0, lds, [&](const uint16_t* stage) {
       if (active) compute_stage(stage, p.k - kt * G::BK, tm, tn, acc);
       ++kt;
-    }, on_start);
+    }, on_start, stamps);
     after_k_loop();
 
-    if (!active) return;
+    if (!active) {
+      stamps.wave_done();
+      return;
+    }
     const bool use_c = p.c != nullptr && p.beta != 0.0f;
     g_cf32_t* cptr = (g_cf32_t*)p.c;
     g_f32_t* dptr = (g_f32_t*)p.d;
@@ -591,6 +598,7 @@ struct FmaTile {
         if (col < p.n) dptr[(int64_t)row * p.ldd + col] = epilogue_value(acc[i][j], cv[j], p.alpha, use_c ? p.beta : 0.0f);
       }
     }
+    stamps.wave_done();
   }
 };
 
@@ -617,25 +625,26 @@ struct KernelLds<S, true> {
 // Computes the work tile at (m0, n0): in the edge class its extent inside the
 // problem selects (KernelShape::CLASSES), else in the kernel's own form.  The
 // class is uniform across the workgroup (scalar descriptor and origin).
-template <class S, int PATH, bool WIDE, class OnStart, class AfterKLoop>
+template <class S, int PATH, bool WIDE, class OnStart, class AfterKLoop, class Stamps = NoStamps>
 __device__ __forceinline__ void run_work_tile(const gg_device_problem_desc& p, int m0, int n0, uint16_t* lds,
-                                              OnStart&& on_start, AfterKLoop&& after_k_loop) {
+                                              OnStart&& on_start, AfterKLoop&& after_k_loop,
+                                              const Stamps& stamps = Stamps{}) {
   if constexpr (PATH == GGK_PATH_MFMA && !WIDE && S::CLASSES) {
     const bool rows = p.m - m0 <= S::G::BM / 2;
     const bool cols = p.n - n0 <= S::G::BN / 2;
     // The full form first: its code then follows the dispatch as it would
     // without the edge classes.
     if (__builtin_expect(!rows && !cols, 1)) {
-      TileFor<S, PATH>::type::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
+      TileFor<S, PATH>::type::template run<false>(p, m0, n0, lds, on_start, after_k_loop, stamps);
     } else if (!cols) {
-      MfmaTile<typename S::GR, S::WAVE_M_R>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
+      MfmaTile<typename S::GR, S::WAVE_M_R>::template run<false>(p, m0, n0, lds, on_start, after_k_loop, stamps);
     } else if (!rows) {
-      MfmaTile<typename S::GC, S::WAVE_M_C>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
+      MfmaTile<typename S::GC, S::WAVE_M_C>::template run<false>(p, m0, n0, lds, on_start, after_k_loop, stamps);
     } else {
-      MfmaTile<typename S::GRC, S::WAVE_M_RC>::template run<false>(p, m0, n0, lds, on_start, after_k_loop);
+      MfmaTile<typename S::GRC, S::WAVE_M_RC>::template run<false>(p, m0, n0, lds, on_start, after_k_loop, stamps);
     }
   } else {
-    TileFor<S, PATH>::type::template run<WIDE>(p, m0, n0, lds, on_start, after_k_loop);
+    TileFor<S, PATH>::type::template run<WIDE>(p, m0, n0, lds, on_start, after_k_loop, stamps);
   }
 }
 

@@ -871,7 +871,8 @@ hipError_t GroupedGemmExecutor::run(hipStream_t stream) const {
   return impl_->buffer.note_launch(stream);
 }
 
-hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream) const {
+hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream,
+                                           long long* d_tile_phases) const {
   if (impl_ == nullptr) return hipErrorInvalidDevicePointer;
   if (impl_->failed) return hipErrorInvalidValue;
   if (impl_->total_tiles == 0 || impl_->problem_count == 0) return hipSuccess;
@@ -879,12 +880,16 @@ hipError_t GroupedGemmExecutor::run_traced(int* d_tile_map, long long* d_wg_cloc
       impl_->variant, impl_->path, impl_->addressing, impl_->d_problems, impl_->d_ints,
       impl_->d_ints + impl_->problem_count + 1, impl_->d_ints + 2 * (impl_->problem_count + 1), impl_->d_work_table(),
       impl_->problem_count, impl_->launch_total, impl_->d_state, impl_->launch_bounds.data(), impl_->grid_ctas, d_tile_map,
-      d_wg_clock, stream);
+      d_wg_clock, d_tile_phases, stream);
   if (status != hipSuccess) return status;
   return impl_->buffer.note_launch(stream);
 }
 
 int GroupedGemmExecutor::problem_count() const { return impl_ != nullptr ? impl_->problem_count : 0; }
+
+int GroupedGemmExecutor::launched_work_tiles() const {
+  return impl_ != nullptr && !impl_->failed ? impl_->launch_total : 0;
+}
 
 int GroupedGemmExecutor::total_tiles() const { return impl_ != nullptr ? impl_->total_tiles : 0; }
 

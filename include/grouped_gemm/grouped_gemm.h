@@ -155,8 +155,14 @@ class GroupedGemmExecutor {
   int grid_ctas() const;
 
   // Additions for measurement and parity checks.  run_traced() runs the same
-  // scheduler with instrumentation (see ggk_launch_grouped_traced).
-  hipError_t run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream = nullptr) const;
+  // scheduler with instrumentation (see ggk_launch_grouped_traced);
+  // d_tile_phases holds GGK_PHASE_COUNT int64s per launched work tile
+  // (launched_work_tiles()).
+  hipError_t run_traced(int* d_tile_map, long long* d_wg_clock, hipStream_t stream = nullptr,
+                        long long* d_tile_phases = nullptr) const;
+  // Work-tile indices one launch claims: the work tiles, with the row halves
+  // the work table lists counted one each.
+  int launched_work_tiles() const;
   bool using_tensor_cores() const;
   // The schedule build() planned: the work-tile shape of the kernel it chose,
   // the scheduling order (sorted position at each scheduling position), the

@@ -115,9 +115,11 @@ int gg_executor_build(gg_executor* executor, const gg_problem_desc* sorted_probl
                       const gg_kernel_config* config);
 /* run (src/grouped_gemm.cu:1241-1265); stream is a hipStream_t (NULL: default). */
 int gg_executor_run(const gg_executor* executor, hipStream_t stream);
-/* Instrumented run, see ggk_launch_grouped_traced. */
+/* Instrumented run, see ggk_launch_grouped_traced (d_tile_phases may be NULL). */
 int gg_executor_run_traced(const gg_executor* executor, int* d_tile_map, long long* d_wg_clock,
-                           hipStream_t stream);
+                           long long* d_tile_phases, hipStream_t stream);
+/* GroupedGemmExecutor::launched_work_tiles (no reference counterpart). */
+int gg_executor_launched_work_tiles(const gg_executor* executor);
 int gg_executor_problem_count(const gg_executor* executor);
 int gg_executor_total_tiles(const gg_executor* executor);
 int gg_executor_grid_ctas(const gg_executor* executor);

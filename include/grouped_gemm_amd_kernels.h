@@ -238,12 +238,29 @@ hipError_t ggk_launch_grouped(int variant, int path, int addressing, const gg_de
  * receive (problem, tile_m, tile_n), problem in sorted order, and no
  * GEMM is computed.  d_wg_clock (may be NULL): for workgroup w, the 100 MHz
  * wall clock at its start and at the end of its last tile go to [2w, 2w+2);
- * the GEMM is computed as usual. */
+ * the GEMM is computed as usual.  d_tile_phases (may be NULL; zeroed by the
+ * caller): for work-tile index t (of total_work), GGK_PHASE_COUNT int64s at
+ * [GGK_PHASE_COUNT t, ...) receive its phase stamps (GGK_PHASE_*); the GEMM
+ * is computed as usual.  No reference counterpart: measurement only. */
+enum {
+  GGK_PHASE_WALL = 0,         /* 100 MHz wall clock at the work tile's start */
+  GGK_PHASE_START = 1,        /* core clock (s_memtime) at its start */
+  GGK_PHASE_FIRST_STAGE = 2,  /* the first stage's loads of one wave have landed */
+  GGK_PHASE_K_LOOP = 3,       /* every wave has its first stage: the k-loop starts */
+  GGK_PHASE_K_END = 4,        /* the k-loop has ended (before the hand-over of the next index) */
+  GGK_PHASE_EPILOGUE = 5,     /* the hand-over is done: the epilogue starts */
+  GGK_PHASE_EPILOGUE_END = 6, /* the last wave has issued its epilogue (latest over the waves) */
+  GGK_PHASE_WHO = 7,          /* workgroup | half << 20 (0 whole, 1 / 2 a row half) | rows << 22 |
+                                 cols << 34 | stages << 46: the tile's rows and columns inside its
+                                 problem (at most the work tile's), its k-stages */
+  GGK_PHASE_COUNT = 8
+};
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,
                                      const int* d_work_offsets, const int* d_order, const int* d_work_table,
                                      int problem_count, int total_work, int* d_state, const int* chunk_bounds,
-                                     int grid, int* d_tile_map, long long* d_wg_clock, hipStream_t stream);
+                                     int grid, int* d_tile_map, long long* d_wg_clock, long long* d_tile_phases,
+                                     hipStream_t stream);
 
 /* Device-resident preparation of a mixture-of-experts group (no reference
  * counterpart: it is the step before the grouped launch in MoE use, done here

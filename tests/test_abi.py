@@ -138,7 +138,8 @@ def test_failed_build_blocks_run():
         offs = (ctypes.c_int * 2)(0, 1)
         assert lib.gg_executor_build(ex, probs, 1, offs, 2, 1, ctypes.byref(bad_cfg)) == _lib.HIP_ERROR_INVALID_VALUE
         assert lib.gg_executor_run(ex, None) == _lib.HIP_ERROR_INVALID_VALUE
-        assert lib.gg_executor_run_traced(ex, None, None, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_run_traced(ex, None, None, None, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert lib.gg_executor_launched_work_tiles(ex) == 0
         assert lib.gg_executor_total_tiles(ex) == 0 and lib.gg_executor_problem_count(ex) == 0
         # a NULL problem list with a non-zero count and a NULL config are rejected the same way
         assert lib.gg_executor_build(ex, None, 3, offs, 2, 1, ctypes.byref(bad_cfg)) != _lib.HIP_SUCCESS

@@ -215,7 +215,7 @@ def _traced_map_by_search(torch, ex, prep, cfg):
     st = _lib.lib().ggk_launch_grouped_traced(_variant_of(cfg, shape), _lib.GGK_PATH_MFMA, _lib.GGK_ADDR_32,
                                               d_desc.data_ptr(), d_tiles.data_ptr(), d_work.data_ptr(),
                                               d_order.data_ptr(), None, count, offsets[-1], d_state.data_ptr(),
-                                              c_bounds, ex.grid_ctas(), tmap.data_ptr(), None, None)
+                                              c_bounds, ex.grid_ctas(), tmap.data_ptr(), None, None, None)
     assert st == 0
     torch.cuda.synchronize()
     return tmap.cpu().numpy()[:3 * total].reshape(total, 3)
@@ -869,6 +869,40 @@ def test_wall_clock_trace(torch):
     c = clock.cpu().numpy().reshape(-1, 2)
     assert (c[:, 0] > 0).all() and (c[:, 1] >= c[:, 0]).all()
     assert c[:, 1].max() - c[:, 0].min() < 100_000_000  # under a second at 100 MHz
+
+
+@pytest.mark.parametrize("name", ["mixed512", "plumbing16"])
+def test_tile_phase_stamps(torch, name):
+    """A traced launch with a phase buffer computes the same D bits as run() and stamps every
+    launched work tile once, its phases in order (start <= first stage <= k-loop <= k-loop end <=
+    epilogue <= last epilogue end), by a workgroup of the grid."""
+    spec = make_spec(name)
+    dw = DeviceWorkload(spec)
+    cfg = KernelConfig.named("128x64x32")
+    ex = GroupedGemmExecutor()
+    assert ex.build(api.prepare_problem_set(dw.problems(), cfg, SortMode.kByTiles), cfg) == 0
+    dw.poison_d()
+    assert ex.run() == 0
+    torch.cuda.synchronize()
+    want = dw.d.clone()
+    n = ex.launched_work_tiles()
+    assert n >= 1
+    phases = torch.zeros(_lib.GGK_PHASE_COUNT * n, dtype=torch.int64, device="cuda")
+    dw.poison_d()
+    assert ex.run_traced(0, 0, None, phases.data_ptr()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dw.d.view(torch.int32), want.view(torch.int32)), "stamped run changed D"
+    ph = phases.cpu().numpy().reshape(n, _lib.GGK_PHASE_COUNT)
+    assert (ph[:, _lib.GGK_PHASE_START] > 0).all(), "a launched work tile was not stamped"
+    order = [_lib.GGK_PHASE_START, _lib.GGK_PHASE_FIRST_STAGE, _lib.GGK_PHASE_K_LOOP, _lib.GGK_PHASE_K_END,
+             _lib.GGK_PHASE_EPILOGUE, _lib.GGK_PHASE_EPILOGUE_END]
+    for a, b in zip(order, order[1:]):
+        assert (ph[:, a] <= ph[:, b]).all(), (a, b)
+    wg = ph[:, _lib.GGK_PHASE_WHO] & 0xFFFFF
+    assert ((wg >= 0) & (wg < ex.grid_ctas())).all()
+    say(f"{name}: {n} work tiles stamped, mean k-loop share "
+        f"{float(np.mean((ph[:, 4] - ph[:, 3]) / np.maximum(ph[:, 6] - ph[:, 1], 1))):.3f}")
+    ex.close()
 
 
 def test_cpp_dropin_driver(torch):

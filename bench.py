@@ -729,6 +729,9 @@ def main() -> int:
                     "frac": round(mfma_frac, 4), "traffic": round(traffic["bytes"]) if traffic else None}
     if traffic:
         roofline["traffic_source"] = f"{traffic['source']} ({traffic['mode']})"
+        # FETCH_SIZE / WRITE_SIZE count what L2 moves to and from the data fabric: requests the
+        # 256 MB MALL serves count as fetched, and no counter here tells them from DRAM reads.
+        roofline["traffic_counts"] = "L2 <-> fabric bytes (MALL hits included)"
         roofline["algorithmic_bytes"] = algo_bytes
     out = {
         "metric": "grouped TFLOP/s + % FP16 MFMA peak on mixed-512, 1 MI355X; tail_share",

@@ -25,6 +25,7 @@ GGK_VARIANT_64x128x32 = 2
 GGK_VARIANT_128x64x32_SMALL = 3  # 128x64x32 on 128 x 128 work tiles (launches with few work tiles)
 GGK_VARIANT_64x128x32_SMALL = 4  # 64x128x32 on 128 x 128 work tiles
 GGK_VARIANT_64x64x16_SMALL = 5  # 64x64x16 on 128 x 128 work tiles
+GGK_VARIANT_COUNT = 6
 GGK_PATH_FMA = 0
 GGK_PATH_MFMA = 1
 GGK_KERNEL_GROUPED = 0
@@ -34,6 +35,7 @@ GGK_ADDR_64 = 1
 GGK_SCHEDULER_CHUNKS = 8
 GGK_SCHEDULER_COUNTER_STRIDE = 32
 GGK_SCHEDULER_STATE_INTS = GGK_SCHEDULER_COUNTER_STRIDE * (GGK_SCHEDULER_CHUNKS + 1)
+GGK_WORK_HALF_SHIFT = 28  # work-table entry: local work tile | (1: first, 2: second half of rows) << shift
 GGK_PHASE_WALL, GGK_PHASE_START, GGK_PHASE_FIRST_STAGE, GGK_PHASE_K_LOOP = 0, 1, 2, 3
 GGK_PHASE_K_END, GGK_PHASE_EPILOGUE, GGK_PHASE_EPILOGUE_END, GGK_PHASE_WHO = 4, 5, 6, 7
 GGK_PHASE_COUNT = 8
@@ -103,6 +105,17 @@ class GGKWorkShape(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int) for name in ("tiles_m", "tiles_n", "threads", "rows", "stage_k")]
 
 
+class GGLaunchPlan(ctypes.Structure):
+    """gg_launch_plan (grouped_gemm_amd.h)"""
+    _fields_ = [
+        ("variant", ctypes.c_int), ("path", ctypes.c_int), ("addressing", ctypes.c_int), ("work", GGKWorkShape),
+        ("total_work", ctypes.c_int), ("launch_total", ctypes.c_int), ("table_ints", ctypes.c_int),
+        ("grid", ctypes.c_int), ("halves", ctypes.c_int),
+        ("chunk_bounds", ctypes.c_int * (GGK_SCHEDULER_CHUNKS + 1)),
+        ("launch_bounds", ctypes.c_int * (GGK_SCHEDULER_CHUNKS + 1)),
+    ]
+
+
 class GGKMoeLayout(ctypes.Structure):
     """ggk_moe_layout (grouped_gemm_amd_kernels.h)"""
     _fields_ = [
@@ -144,6 +157,8 @@ SIGNATURES = {
     "gg_run_baseline_per_problem": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _vp]),
     "gg_count_non_empty_problems": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig)]),
     "gg_grid_ctas_for": (_i, [_P(GGKernelConfig), _i]),
+    "gg_plan_launch": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _i, c_int_p, _P(GGLaunchPlan), c_int_p,
+                            c_int_p, c_int_p, _i]),
     "gg_moe_create": (_i, [_P(GGKMoeLayout), _P(GGKernelConfig), _i, _P(_vp)]),
     "gg_moe_run": (_i, [_vp, _vp, _vp]),
     "gg_moe_grid_ctas": (_i, [_vp]),

@@ -336,6 +336,47 @@ def grid_ctas_for(config: KernelConfig, total_tiles: int) -> int:
     return value
 
 
+@dataclass
+class LaunchPlan:
+    """gg_launch_plan plus its arrays: what GroupedGemmExecutor.build() plans for a sorted set."""
+    variant: int
+    path: int
+    addressing: int
+    work: tuple  # (tiles_m, tiles_n, threads, rows, stage_k) of the work tile
+    total_work: int
+    launch_total: int
+    grid: int
+    halves: bool
+    order: list
+    work_offsets: list
+    chunk_bounds: list
+    work_table: list  # (problem, work tile | half << GGK_WORK_HALF_SHIFT) pairs, flattened
+    launch_bounds: list
+
+
+def plan_launch(sorted_problems: Sequence[ProblemDesc], config: KernelConfig, compute_units: int,
+                blocks_per_cu: Sequence[int]) -> LaunchPlan:
+    """The launch plan build() makes (no reference counterpart), from plain device values:
+    compute_units CUs and blocks_per_cu[v] resident workgroups per CU of variant v.  Host only."""
+    count = len(sorted_problems)
+    arr = _problem_array(sorted_problems)
+    blocks = (ctypes.c_int * _lib.GGK_VARIANT_COUNT)(*blocks_per_cu)
+    plan = _lib.GGLaunchPlan()
+    order = (ctypes.c_int * max(1, count))()
+    offsets = (ctypes.c_int * (count + 1))()
+    cfg = config.to_c()
+    _lib.check(_lib.lib().gg_plan_launch(arr, count, ctypes.byref(cfg), compute_units, blocks, ctypes.byref(plan),
+                                         order, offsets, None, 0), "gg_plan_launch")
+    table = (ctypes.c_int * max(1, plan.table_ints))()
+    _lib.check(_lib.lib().gg_plan_launch(arr, count, ctypes.byref(cfg), compute_units, blocks, ctypes.byref(plan),
+                                         None, None, table, plan.table_ints), "gg_plan_launch")
+    w = plan.work
+    return LaunchPlan(plan.variant, plan.path, plan.addressing, (w.tiles_m, w.tiles_n, w.threads, w.rows, w.stage_k),
+                      plan.total_work, plan.launch_total, plan.grid, bool(plan.halves), list(order)[:count],
+                      list(offsets), list(plan.chunk_bounds), list(table)[:plan.table_ints],
+                      list(plan.launch_bounds))
+
+
 def total_flops(problems: Sequence[ProblemDesc]) -> float:
     """sum of 2*m*n*k (bench/benchmark_grouped_gemm.cu:570-576)."""
     return float(sum(2.0 * p.m * p.n * p.k for p in problems))

@@ -288,6 +288,51 @@ int gg_grid_ctas_for(const gg_kernel_config* config, int total_tiles) {
   return gg::grid_ctas_for(total_tiles, cfg, o);
 }
 
+int gg_plan_launch(const gg_problem_desc* sorted_problems, int count, const gg_kernel_config* config,
+                   int compute_units, const int* blocks_per_cu, gg_launch_plan* plan, int* order,
+                   int* work_offsets, int* table, int table_capacity) {
+  if (config == nullptr || plan == nullptr || blocks_per_cu == nullptr || bad_list(sorted_problems, count)) {
+    return hipErrorInvalidValue;
+  }
+  *plan = gg_launch_plan{};
+  try {
+    const gg::KernelConfig cfg = to_cpp(*config);
+    std::vector<gg::DeviceProblemDesc> problems;
+    problems.reserve(count);
+    for (int i = 0; i < count; ++i) problems.push_back(gg::to_device_problem(to_cpp(sorted_problems[i]), cfg));
+    gg::LaunchPlan p;
+    const hipError_t status = gg::plan_launch(
+        problems, cfg, compute_units,
+        [blocks_per_cu](int variant, int, int* blocks) {
+          if (variant < 0 || variant >= GGK_VARIANT_COUNT) return hipErrorInvalidValue;
+          *blocks = blocks_per_cu[variant];
+          return hipSuccess;
+        },
+        &p);
+    if (status != hipSuccess) return status;
+    plan->variant = p.variant;
+    plan->path = p.path;
+    plan->addressing = p.addressing;
+    plan->work = p.work;
+    plan->total_work = p.total_work;
+    plan->launch_total = p.launch_total;
+    plan->table_ints = static_cast<int>(p.work_table.size());
+    plan->grid = p.grid;
+    plan->halves = p.halves ? 1 : 0;
+    std::copy(p.chunk_bounds.begin(), p.chunk_bounds.end(), plan->chunk_bounds);
+    std::copy(p.launch_bounds.begin(), p.launch_bounds.end(), plan->launch_bounds);
+    if (order != nullptr) std::copy(p.order.begin(), p.order.end(), order);
+    if (work_offsets != nullptr) std::copy(p.work_offsets.begin(), p.work_offsets.end(), work_offsets);
+    if (table != nullptr) {
+      if (table_capacity < plan->table_ints) return hipErrorInvalidValue;
+      std::copy(p.work_table.begin(), p.work_table.end(), table);
+    }
+    return hipSuccess;
+  } catch (...) {
+    return hipErrorOutOfMemory;
+  }
+}
+
 int gg_moe_create(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode, gg_moe** out) {
   if (out == nullptr) return hipErrorInvalidValue;
   *out = nullptr;

@@ -666,6 +666,130 @@ int work_tile_row(int local, int wtm, int wtn) {
 
 }  // namespace
 
+hipError_t plan_launch(const std::vector<DeviceProblemDesc>& problems, const KernelConfig& config,
+                       int compute_units, const BlocksPerCu& blocks_per_cu, LaunchPlan* plan) {
+  if (plan == nullptr) return hipErrorInvalidValue;
+  *plan = LaunchPlan{};
+  const int base_variant = resolve_variant(config);
+  if (base_variant < 0 || compute_units < 1 || !blocks_per_cu) return hipErrorInvalidValue;
+  const int count = static_cast<int>(problems.size());
+  for (const DeviceProblemDesc& p : problems) {
+    if (p.m < 0 || p.n < 0 || p.k < 0) return hipErrorInvalidValue;
+    const bool live = p.m > 0 && p.n > 0;
+    if (p.tiles_m != (live ? ceil_div(p.m, config.cta_m) : 0) || p.tiles_n != (live ? ceil_div(p.n, config.cta_n) : 0)) {
+      return hipErrorInvalidValue;
+    }
+  }
+  int variant = base_variant;
+  const int path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;
+  ggk_work_shape shape{};
+  hipError_t status = ggk_work_shape_get(variant, path, &shape);
+  if (status != hipSuccess) return status;
+
+  // A launch with few work tiles is bound by the latency of each tile's
+  // stages rather than by bandwidth: when the 128 x 128 work tiles of the
+  // small-set variants number at most two per workgroup slot (two
+  // workgroups per CU), the set runs on those instead of the 256 x 256 ones.
+  // The reference tile map is the same either way.
+  const int small_variant = ggk_small_variant(variant);
+  if (path == GGK_PATH_MFMA && small_variant >= 0) {
+    ggk_work_shape small{};
+    status = ggk_work_shape_get(small_variant, path, &small);
+    if (status != hipSuccess) return status;
+    int64_t work = 0;
+    for (const DeviceProblemDesc& p : problems) {
+      work += static_cast<int64_t>(ceil_div(p.tiles_m, small.tiles_m)) * ceil_div(p.tiles_n, small.tiles_n);
+    }
+    if (work <= GG_SMALL_SET_TILES_PER_CU * static_cast<int64_t>(compute_units)) {
+      variant = small_variant;
+      shape = small;
+    }
+  }
+  auto addressing_for = [&](int v) {
+    for (const DeviceProblemDesc& p : problems) {
+      if (ggk_needs_addr64(v, path, &p) == 1) return GGK_ADDR_64;
+    }
+    return GGK_ADDR_32;
+  };
+  int addressing = addressing_for(variant);
+  // The 64-bit form of the 256 x 256 work tile spills registers: a set that
+  // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
+  if (addressing == GGK_ADDR_64 && path == GGK_PATH_MFMA && ggk_small_variant(variant) >= 0) {
+    variant = ggk_small_variant(variant);
+    status = ggk_work_shape_get(variant, path, &shape);
+    if (status != hipSuccess) return status;
+    addressing = addressing_for(variant);
+  }
+
+  std::vector<int> work(count);
+  for (int i = 0; i < count; ++i) {
+    // Never above the problem's tile count, so the sums fit an int.
+    work[i] = ceil_div(problems[i].tiles_m, shape.tiles_m) * ceil_div(problems[i].tiles_n, shape.tiles_n);
+  }
+  const int bm = config.cta_m * shape.tiles_m;
+  Schedule schedule = plan_schedule(problems, work, bm, config.cta_n * shape.tiles_n, shape.stage_k);
+  const int total_work = schedule.work_offsets.back();
+  const bool work_table = total_work > 0 && total_work <= kWorkTableMax;
+
+  int blocks = 0;
+  status = blocks_per_cu(variant, path, &blocks);
+  if (status != hipSuccess) return status;
+  OccupancyInfo occupancy{};
+  occupancy.sm_count = compute_units;
+  occupancy.active_blocks_per_sm = blocks;
+  // The persistent grid is sized by the units it claims: work tiles.
+  const int grid = grid_ctas_for(total_work, config, occupancy);
+
+  // The work table in claim order: (problem, work tile within it) of every
+  // work-tile index, so that the kernel reads it with one load instead of
+  // searching.  Within the last kTailHalves entries of each chunk, a work tile
+  // with more than half its rows inside the problem is listed as its two
+  // halves, consecutively.
+  std::vector<int> table;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds = schedule.bounds;
+  bool halves = false;
+  if (work_table) {
+    halves = kTailHalves > 0 && ggk_work_halves_supported(variant, path) == 1 &&
+             total_work <= kTailHalvesMaxPerSlot * grid && planned_idle_share(schedule, grid) >= kTailHalvesMinIdle;
+    table.reserve(2 * static_cast<size_t>(total_work) + 4 * GGK_SCHEDULER_CHUNKS * std::max(kTailHalves, 0));
+    int index = 0;  // work-tile index of the entry being listed
+    int chunk = 0;
+    launch_bounds[0] = 0;
+    for (const int prob : schedule.order) {
+      const DeviceProblemDesc& dp = problems[prob];
+      const int wtm = ceil_div(dp.tiles_m, shape.tiles_m);
+      const int wtn = ceil_div(dp.tiles_n, shape.tiles_n);
+      for (int w = 0; w < work[prob]; ++w, ++index) {
+        while (chunk < GGK_SCHEDULER_CHUNKS && index >= schedule.bounds[chunk + 1]) {
+          launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
+        }
+        const bool tail = halves && index >= schedule.bounds[chunk + 1] - kTailHalves;
+        if (tail && dp.m - work_tile_row(w, wtm, wtn) * bm > bm / 2) {
+          table.insert(table.end(), {prob, w | (1 << GGK_WORK_HALF_SHIFT), prob, w | (2 << GGK_WORK_HALF_SHIFT)});
+        } else {
+          table.insert(table.end(), {prob, w});
+        }
+      }
+    }
+    while (chunk < GGK_SCHEDULER_CHUNKS) launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
+  }
+
+  plan->variant = variant;
+  plan->path = path;
+  plan->addressing = addressing;
+  plan->work = shape;
+  plan->order = std::move(schedule.order);
+  plan->work_offsets = std::move(schedule.work_offsets);
+  plan->chunk_bounds = schedule.bounds;
+  plan->launch_total = work_table ? static_cast<int>(table.size() / 2) : total_work;
+  plan->work_table = std::move(table);
+  plan->launch_bounds = launch_bounds;
+  plan->total_work = total_work;
+  plan->grid = grid;
+  plan->halves = halves;
+  return hipSuccess;
+}
+
 GroupedGemmExecutor::GroupedGemmExecutor() : impl_(new Impl()) {}
 
 GroupedGemmExecutor::~GroupedGemmExecutor() {
@@ -713,30 +837,6 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   if (prepared.tile_offsets.back() != prepared.total_tiles) return hipErrorInvalidValue;
   if (prepared.tile_offsets[0] != 0) return hipErrorInvalidValue;
 
-  // A launch with few work tiles is bound by the latency of each tile's
-  // stages rather than by bandwidth: when the 128 x 128 work tiles of the
-  // small-set variants number at most two per workgroup slot (two
-  // workgroups per CU), the set runs on those instead of the 256 x 256 ones.
-  // The reference tile map is the same either way.
-  const int small_variant = ggk_small_variant(mode.variant);
-  if (mode.path == GGK_PATH_MFMA && small_variant >= 0) {
-    ggk_work_shape small{};
-    status = ggk_work_shape_get(small_variant, mode.path, &small);
-    if (status != hipSuccess) return status;
-    int64_t work = 0;
-    for (int i = 0; i < problem_count; ++i) {
-      const ProblemDesc& p = prepared.sorted_problems[i];
-      if (p.m <= 0 || p.n <= 0) continue;
-      work += static_cast<int64_t>(ceil_div(ceil_div(p.m, config.cta_m), small.tiles_m)) *
-              ceil_div(ceil_div(p.n, config.cta_n), small.tiles_n);
-    }
-    if (work <= GG_SMALL_SET_TILES_PER_CU * static_cast<int64_t>(mode.device.compute_units)) {
-      mode.variant = small_variant;
-      mode.work = small;
-    }
-  }
-
-  int addressing = GGK_ADDR_32;
   std::vector<DeviceProblemDesc> device_problems;
   device_problems.reserve(problem_count);
   for (int i = 0; i < problem_count; ++i) {
@@ -748,75 +848,29 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
     if (static_cast<int64_t>(prepared.tile_offsets[i + 1]) - prepared.tile_offsets[i] != tiles) {
       return hipErrorInvalidValue;
     }
-    if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) addressing = GGK_ADDR_64;
     device_problems.push_back(dp);
   }
-  // The 64-bit form of the 256 x 256 work tile spills registers: a set that
-  // needs it runs on 128 x 128 work tiles of the same macro-tile (same D).
-  if (addressing == GGK_ADDR_64 && mode.path == GGK_PATH_MFMA && ggk_small_variant(mode.variant) >= 0) {
-    mode.variant = ggk_small_variant(mode.variant);
-    status = ggk_work_shape_get(mode.variant, mode.path, &mode.work);
-    if (status != hipSuccess) return status;
-    addressing = GGK_ADDR_32;
-    for (const DeviceProblemDesc& dp : device_problems) {
-      if (ggk_needs_addr64(mode.variant, mode.path, &dp) == 1) addressing = GGK_ADDR_64;
-    }
-  }
-  std::vector<int> work(problem_count);
-  for (int i = 0; i < problem_count; ++i) {
-    // Never above the problem's tile count, so the sums fit an int.
-    const DeviceProblemDesc& dp = device_problems[i];
-    work[i] = ceil_div(dp.tiles_m, mode.work.tiles_m) * ceil_div(dp.tiles_n, mode.work.tiles_n);
-  }
-  const Schedule schedule = plan_schedule(device_problems, work, config.cta_m * mode.work.tiles_m,
-                                          config.cta_n * mode.work.tiles_n, mode.work.stage_k);
-  const int total_work = schedule.work_offsets.back();
-  const bool work_table = total_work > 0 && total_work <= kWorkTableMax;
-
-  OccupancyInfo occupancy{};
-  status = cached_occupancy(config, mode, &occupancy);
+  // The variant, schedule, grid and work table, with the occupancy of the
+  // variant the plan chooses.
+  LaunchPlan plan;
+  status = plan_launch(device_problems, config, mode.device.compute_units,
+                       [&](int variant, int path, int* blocks) {
+                         RuntimeMode chosen = mode;
+                         chosen.variant = variant;
+                         chosen.path = path;
+                         hipError_t s = ggk_work_shape_get(variant, path, &chosen.work);
+                         if (s != hipSuccess) return s;
+                         OccupancyInfo occupancy{};
+                         s = cached_occupancy(config, chosen, &occupancy);
+                         *blocks = occupancy.active_blocks_per_sm;
+                         return s;
+                       },
+                       &plan);
   if (status != hipSuccess) return status;
-  // The persistent grid is sized by the units it claims: work tiles.
-  const int grid_slots = grid_ctas_for(total_work, config, occupancy);
+  const std::vector<int>& table = plan.work_table;
 
   // Device ints: the reference tile offsets (sorted order), the work-tile
-  // offsets (scheduling order), the scheduling order, then the work table --
-  // (problem, work tile within it) of every work-tile index, so that the
-  // kernel reads it with one load instead of searching.
-  // The work table in claim order.  Within the last kTailHalves entries of
-  // each chunk, a work tile with more than half its rows inside the problem
-  // is listed as its two halves, consecutively.
-  std::vector<int> table;
-  std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds = schedule.bounds;
-  if (work_table) {
-    const bool halves = kTailHalves > 0 && ggk_work_halves_supported(mode.variant, mode.path) == 1 &&
-                        total_work <= kTailHalvesMaxPerSlot * grid_slots &&
-                        planned_idle_share(schedule, grid_slots) >= kTailHalvesMinIdle;
-    const int bm = config.cta_m * mode.work.tiles_m;
-    table.reserve(2 * static_cast<size_t>(total_work) + 4 * GGK_SCHEDULER_CHUNKS * std::max(kTailHalves, 0));
-    int index = 0;  // work-tile index of the entry being listed
-    int chunk = 0;
-    launch_bounds[0] = 0;
-    for (const int prob : schedule.order) {
-      const DeviceProblemDesc& dp = device_problems[prob];
-      const int wtm = ceil_div(dp.tiles_m, mode.work.tiles_m);
-      const int wtn = ceil_div(dp.tiles_n, mode.work.tiles_n);
-      for (int w = 0; w < work[prob]; ++w, ++index) {
-        while (chunk < GGK_SCHEDULER_CHUNKS && index >= schedule.bounds[chunk + 1]) {
-          launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
-        }
-        const bool tail = halves && index >= schedule.bounds[chunk + 1] - kTailHalves;
-        if (tail && dp.m - work_tile_row(w, wtm, wtn) * bm > bm / 2) {
-          table.insert(table.end(), {prob, w | (1 << GGK_WORK_HALF_SHIFT), prob, w | (2 << GGK_WORK_HALF_SHIFT)});
-        } else {
-          table.insert(table.end(), {prob, w});
-        }
-      }
-    }
-    while (chunk < GGK_SCHEDULER_CHUNKS) launch_bounds[++chunk] = static_cast<int>(table.size() / 2);
-  }
-  const int launch_total = work_table ? static_cast<int>(table.size() / 2) : total_work;
-
+  // offsets (scheduling order), the scheduling order, then the work table.
   const size_t int_count = 3 * static_cast<size_t>(problem_count) + 2 + table.size();
   const size_t desc_bytes = DeviceBuffer::round256(problem_count * sizeof(DeviceProblemDesc));
   const size_t int_bytes = DeviceBuffer::round256(int_count * sizeof(int));
@@ -826,8 +880,8 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   if (problem_count > 0) std::memcpy(host.data(), device_problems.data(), problem_count * sizeof(DeviceProblemDesc));
   int* ints = reinterpret_cast<int*>(host.data() + desc_bytes);
   ints = std::copy(prepared.tile_offsets.begin(), prepared.tile_offsets.end(), ints);
-  ints = std::copy(schedule.work_offsets.begin(), schedule.work_offsets.end(), ints);
-  ints = std::copy(schedule.order.begin(), schedule.order.end(), ints);
+  ints = std::copy(plan.work_offsets.begin(), plan.work_offsets.end(), ints);
+  ints = std::copy(plan.order.begin(), plan.order.end(), ints);
   ints = std::copy(table.begin(), table.end(), ints);
 
   status = impl_->buffer.reserve(total_bytes);
@@ -841,16 +895,16 @@ hipError_t GroupedGemmExecutor::build(const PreparedProblemSet& prepared, const 
   impl_->d_state = reinterpret_cast<int*>(base + desc_bytes + int_bytes);
   impl_->problem_count = problem_count;
   impl_->total_tiles = prepared.total_tiles;
-  impl_->total_work = total_work;
+  impl_->total_work = plan.total_work;
   impl_->config = config;
-  impl_->variant = mode.variant;
-  impl_->path = mode.path;
-  impl_->addressing = addressing;
-  impl_->chunk_bounds = schedule.bounds;
-  impl_->work_table = work_table;
-  impl_->launch_total = launch_total;
-  impl_->launch_bounds = launch_bounds;
-  impl_->grid_ctas = grid_slots;
+  impl_->variant = plan.variant;
+  impl_->path = plan.path;
+  impl_->addressing = plan.addressing;
+  impl_->chunk_bounds = plan.chunk_bounds;
+  impl_->work_table = !table.empty();
+  impl_->launch_total = plan.launch_total;
+  impl_->launch_bounds = plan.launch_bounds;
+  impl_->grid_ctas = plan.grid;
   impl_->failed = false;
   return hipSuccess;
 }

@@ -13,7 +13,9 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime_api.h>
 
+#include <array>
 #include <cstdint>
+#include <functional>
 #include <vector>
 
 #include "grouped_gemm_amd_kernels.h"
@@ -206,6 +208,47 @@ int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& confi
 // max(1, min(sm_count * max(1, active_blocks_per_sm), max(total_tiles, sm_count)));
 // 0 when total_tiles is 0.
 int grid_ctas_for(int total_tiles, const KernelConfig& config, const OccupancyInfo& occupancy);
+
+// Addition with no counterpart in the reference: the launch plan that
+// GroupedGemmExecutor::build() makes for a set of sorted problems, computed
+// from plain values with no device call.
+//  * variant: the configuration's own, or its 128 x 128 work-tile form when
+//    the set has at most 4 such work tiles per CU (compute_units CUs) or
+//    needs 64-bit addressing in the 256 x 256 form; addressing as it needs.
+//  * schedule: order, work_offsets and chunk_bounds as
+//    GroupedGemmExecutor::schedule() reports them.
+//  * grid: grid_ctas_for(total_work) with blocks_per_cu(variant, path)
+//    resident workgroups per CU.
+//  * work_table: (problem, work tile) pairs in claim order, a work tile among
+//    the last of its chunk listed as its two row halves (GGK_WORK_HALF_SHIFT)
+//    when the kernel reads halves and the planned schedule leaves a ragged
+//    end; empty above 2^22 work tiles (the kernel then searches).
+//    launch_total and launch_bounds count its entries (without a table, the
+//    work tiles and chunk_bounds).
+struct LaunchPlan {
+  int variant = -1;
+  int path = -1;
+  int addressing = GGK_ADDR_32;
+  ggk_work_shape work{};
+  std::vector<int> order;
+  std::vector<int> work_offsets;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> chunk_bounds{};
+  std::vector<int> work_table;
+  std::array<int, GGK_SCHEDULER_CHUNKS + 1> launch_bounds{};
+  int total_work = 0;
+  int launch_total = 0;
+  int grid = 0;
+  bool halves = false;
+};
+
+// Resident workgroups per CU of the grouped kernel of (variant, path).
+using BlocksPerCu = std::function<hipError_t(int variant, int path, int* blocks)>;
+
+// hipErrorInvalidValue for a configuration without a kernel, compute_units
+// below 1, a negative extent or tile counts that are not the ceilings of
+// m / cta_m and n / cta_n (zero for an empty problem).
+hipError_t plan_launch(const std::vector<DeviceProblemDesc>& problems, const KernelConfig& config,
+                       int compute_units, const BlocksPerCu& blocks_per_cu, LaunchPlan* plan);
 
 // ---------------------------------------------------------------------------
 // Additions with no counterpart in the reference: the grouped GEMM of a

@@ -146,6 +146,33 @@ int gg_count_non_empty_problems(const gg_problem_desc* problems, int count,
  * device (src/grouped_gemm.cu:1228-1236); negative hipError_t on failure. */
 int gg_grid_ctas_for(const gg_kernel_config* config, int total_tiles);
 
+/* The launch plan that gg_executor_build makes for count sorted problems
+ * (grouped_gemm::plan_launch; no reference counterpart), from plain values
+ * and with no device call: compute_units CUs and blocks_per_cu[v] resident
+ * workgroups per CU of variant v's grouped kernel on the configuration's path
+ * (GGK_VARIANT_COUNT entries).  The problems' pointers are not read.  Writes
+ * *plan, order[count], work_offsets[count + 1] and the work table,
+ * plan->table_ints ints (none for a set above 2^22 work tiles, which the
+ * kernel searches instead), into table[table_capacity]; any array may be
+ * NULL.  hipErrorInvalidValue for a table that does not fit, with *plan
+ * filled. */
+typedef struct gg_launch_plan {
+  int variant;
+  int path;
+  int addressing;
+  ggk_work_shape work;
+  int total_work;   /* work tiles */
+  int launch_total; /* work-tile indices one launch claims */
+  int table_ints;   /* ints of the work table (0: none) */
+  int grid;
+  int halves;       /* 1 when the table lists tail halves */
+  int chunk_bounds[GGK_SCHEDULER_CHUNKS + 1];
+  int launch_bounds[GGK_SCHEDULER_CHUNKS + 1];
+} gg_launch_plan;
+int gg_plan_launch(const gg_problem_desc* sorted_problems, int count, const gg_kernel_config* config,
+                   int compute_units, const int* blocks_per_cu, gg_launch_plan* plan, int* order,
+                   int* work_offsets, int* table, int table_capacity);
+
 /* MoeGroupedGemm (no reference counterpart): a mixture-of-experts group whose
  * problem set is prepared on the device from device-side token counts, see
  * ggk_moe_prepare for the layout.  gg_moe_create checks the layout and

@@ -312,7 +312,26 @@ def test_host_schedule_is_the_longest_first_plan(torch, config, count):
                              [p.c is not None and p.beta != 0.0 for p in prep.sorted_problems])
         say(f"{config} {count} {mode.name}: work shape {shape.tiles_m}x{shape.tiles_n}, {offsets[-1]} work tiles")
         assert (order, offsets, bounds) == want, (config, count, mode)
+        # build() is plan_launch with this device's CU count and occupancies.
+        plan = api.plan_launch(prep.sorted_problems, cfg, *_device_plan_values(cfg))
+        assert (plan.order, plan.work_offsets, plan.chunk_bounds) == (order, offsets, bounds)
+        assert (plan.grid, plan.launch_total) == (ex.grid_ctas(), ex.launched_work_tiles())
+        assert (plan.work[0], plan.work[1]) == (shape.tiles_m, shape.tiles_n)
         ex.close()
+
+
+def _device_plan_values(cfg):
+    """(compute units, resident workgroups per CU of each variant) of the current device, as
+    build() reads them."""
+    info = _lib.GGKDeviceInfo()
+    _lib.check(_lib.lib().ggk_device_info_get(ctypes.byref(info)), "device info")
+    path = _lib.GGK_PATH_MFMA if cfg.use_tensor_cores else _lib.GGK_PATH_FMA
+    blocks = []
+    for v in range(_lib.GGK_VARIANT_COUNT):
+        b = ctypes.c_int(0)
+        _lib.check(_lib.lib().ggk_occupancy(v, path, ctypes.byref(b)), "occupancy")
+        blocks.append(b.value)
+    return info.compute_units, blocks
 
 
 @pytest.mark.parametrize("name", ["one", "four_equal", "two_big", "one_big_among_many"])

@@ -1,6 +1,8 @@
 """Host-side parity of the library, on the CPU: prepare_problem_set (sort permutations, tile offsets,
 total tiles), tile counts, sort-mode names and empty-problem counting must equal the oracle bit for
-bit.  These entry points never touch the GPU."""
+bit, and the executor's launch plan (variant, schedule, grid, work table) its restatement in
+schedule_plan.py.  These entry points never touch the GPU."""
+import ctypes
 import json
 from pathlib import Path
 
@@ -111,3 +113,138 @@ def test_metric_helpers_match_oracle():
     m, n, k = O.bench_shapes("mixed", 256, 42)
     probs = _problems(m, n, k)
     assert api.total_flops(probs) == O.total_flops(m, n, k)
+
+
+def _plan_sets():
+    """Sets that reach each branch of the launch planning: oversized problems cut across chunks
+    (four_big), tail halves (mixed512), zero-tile problems (zeros5000), one tiny problem, the small
+    form (plumbing-sized sets), and no work table (a set above 2^22 work tiles)."""
+    from grouped_gemm_gpu_kernel_amd.workloads import make_spec
+    rng = np.random.default_rng(5)
+    sets = {}
+    for name in ("mixed512", "dense64", "longtail4096", "plumbing16"):
+        spec = make_spec(name)
+        sets[name] = (list(spec.m), list(spec.n), list(spec.k))
+    cnt = 5000
+    mm = rng.integers(0, 300, cnt)
+    mm[rng.random(cnt) < 0.3] = 0
+    sets["zeros5000"] = (list(mm), list(rng.integers(1, 300, cnt)), list(rng.integers(0, 50, cnt)))
+    sets["one"] = ([1], [1], [1])
+    sets["four_big"] = ([2048] * 4 + [100] * 5, [2048] * 4 + [300] * 5, [64] * 4 + [20] * 5)
+    sets["searched"] = ([1 << 20], [1 << 20], [64])
+    return sets
+
+
+def _restated_plan(sorted_problems, cfg, compute_units, blocks, addr64_rows=None):
+    from grouped_gemm_gpu_kernel_amd import _lib
+    import schedule_plan as S
+    base = {(64, 64): _lib.GGK_VARIANT_64x64x16, (128, 64): _lib.GGK_VARIANT_128x64x32,
+            (64, 128): _lib.GGK_VARIANT_64x128x32}[(cfg.cta_m, cfg.cta_n)]
+    path = _lib.GGK_PATH_MFMA if cfg.use_tensor_cores else _lib.GGK_PATH_FMA
+
+    def shape(v):
+        ws = _lib.GGKWorkShape()
+        _lib.check(_lib.lib().ggk_work_shape_get(v, path, ctypes.byref(ws)), "work shape")
+        return ws
+
+    cta = dict(m=cfg.cta_m, n=cfg.cta_n, persistent=cfg.persistent_ctas, variant=base,
+               small=_lib.lib().ggk_small_variant(base))
+    problems = [(p.m, p.n, p.k, p.c is not None and p.beta != 0.0) for p in sorted_problems]
+    return S.plan_launch(problems, cta, cfg.use_tensor_cores, compute_units, blocks,
+                         lambda v: (shape(v).tiles_m, shape(v).tiles_n, shape(v).stage_k),
+                         lambda v: _lib.lib().ggk_work_halves_supported(v, path) == 1,
+                         lambda v: addr64_rows is not None and shape(v).rows >= addr64_rows)
+
+
+def _check_table(plan, sorted_problems, cfg):
+    """Properties that hold whatever the schedule: every work tile of every problem is listed once,
+    whole or as its two halves (consecutive), in the order of the scheduling positions."""
+    if not plan.work_table:
+        assert plan.launch_total == plan.total_work and plan.launch_bounds == plan.chunk_bounds
+        return
+    shift = 28
+    seen = {}
+    entries = list(zip(plan.work_table[0::2], plan.work_table[1::2]))
+    assert len(entries) == plan.launch_total == plan.launch_bounds[-1]
+    i = 0
+    while i < len(entries):
+        prob, code = entries[i]
+        local, half = code & ((1 << shift) - 1), code >> shift
+        if half == 0:
+            seen[(prob, local)] = seen.get((prob, local), 0) + 1
+            i += 1
+            continue
+        assert half == 1 and entries[i + 1] == (prob, local | (2 << shift))
+        seen[(prob, local)] = seen.get((prob, local), 0) + 1
+        i += 2
+    assert set(seen.values()) == {1} and len(seen) == plan.total_work
+    positions = [plan.order.index(p) for p, _ in entries]
+    assert positions == sorted(positions)
+    assert plan.launch_bounds == sorted(plan.launch_bounds) and plan.launch_bounds[0] == 0
+
+
+@pytest.mark.parametrize("config", CONFIGS + ["128x64x32/fma", "128x64x32/persistent100"])
+def test_launch_plan_matches_restatement(config):
+    """GroupedGemmExecutor::build's launch plan (variant, schedule, grid, work table with its tail
+    halves), computed on the host from plain device values (256 CUs; one workgroup per CU of the
+    256 x 256 work-tile kernels, two of the 128 x 128 ones), equals the restatement in
+    tests/schedule_plan.py field for field; the table lists every work tile once."""
+    name, _, extra = config.partition("/")
+    cfg = KernelConfig.named(name, use_tensor_cores=extra != "fma",
+                             persistent_ctas=100 if extra == "persistent100" else 0)
+    blocks = [1, 1, 1, 2, 2, 2]
+    halves_seen = False
+    for set_name, (m, n, k) in _plan_sets().items():
+        probs = _problems(m, n, k)
+        for mode in (SortMode.kNone, SortMode.kByTiles):
+            if set_name == "searched" and mode == SortMode.kByTiles:
+                continue
+            prep = api.prepare_problem_set(probs, cfg, mode)
+            got = api.plan_launch(prep.sorted_problems, cfg, 256, blocks)
+            want = _restated_plan(prep.sorted_problems, cfg, 256, blocks)
+            where = f"{config} {set_name} mode={int(mode)}"
+            assert (got.variant, got.addressing, got.total_work, got.grid, got.halves) == (
+                want["variant"], want["addressing"], want["total_work"], want["grid"], want["halves"]), where
+            assert got.order == want["order"] and got.work_offsets == want["offsets"], where
+            assert got.chunk_bounds == want["bounds"], where
+            assert got.work_table == want["table"], where
+            assert got.launch_total == want["launch_total"] and got.launch_bounds == want["launch_bounds"], where
+            _check_table(got, prep.sorted_problems, cfg)
+            halves_seen |= got.halves
+            if set_name == "searched":
+                assert got.total_work > 1 << 22 and not got.work_table, where
+    if cfg.use_tensor_cores and not cfg.persistent_ctas:
+        assert halves_seen  # mixed512 lists halves
+
+
+def test_launch_plan_64bit_sets_run_on_small_work_tiles():
+    """A set whose row stride needs 64-bit offsets in 256-row work tiles (lda = 5e6: 256 lda > 2^30)
+    but not in 128-row ones runs on the 128 x 128 form with 32-bit addressing."""
+    from grouped_gemm_gpu_kernel_amd import _lib
+    cfg = KernelConfig.named("128x64x32")
+    probs = [ProblemDesc(4096, 4096, 64, 1, 1, None, 1, 5_000_000, 4096, 4096, 4096)]
+    got = api.plan_launch(probs, cfg, 256, [1, 1, 1, 2, 2, 2])
+    want = _restated_plan(probs, cfg, 256, [1, 1, 1, 2, 2, 2], addr64_rows=256)
+    assert got.variant == _lib.GGK_VARIANT_128x64x32_SMALL == want["variant"]
+    assert got.addressing == _lib.GGK_ADDR_32 == want["addressing"]
+    assert got.order == want["order"] and got.work_table == want["table"] and got.grid == want["grid"]
+
+
+def test_launch_plan_rejects_bad_input():
+    from grouped_gemm_gpu_kernel_amd import _lib
+    cfg = KernelConfig.named("128x64x32")
+    probs = _problems([64], [64], [64])
+    for bad_cfg, cus in ((KernelConfig(cta_m=32, cta_n=64, cta_k=16), 256), (cfg, 0)):
+        with pytest.raises(_lib.HipError):
+            api.plan_launch(probs, bad_cfg, cus, [1] * 6)
+    with pytest.raises(_lib.HipError):
+        api.plan_launch(_problems([-1], [64], [64]), cfg, 256, [1] * 6)
+    arr = api._problem_array(probs)
+    plan = _lib.GGLaunchPlan()
+    blocks = (ctypes.c_int * 6)(*([1] * 6))
+    table = (ctypes.c_int * 1)()
+    assert _lib.lib().gg_plan_launch(arr, 1, ctypes.byref(cfg.to_c()), 256, blocks, ctypes.byref(plan), None, None,
+                                     table, 1) == _lib.HIP_ERROR_INVALID_VALUE
+    assert plan.table_ints == 2 and plan.grid == 256
+    assert _lib.lib().gg_plan_launch(arr, 1, ctypes.byref(cfg.to_c()), 256, None, ctypes.byref(plan), None, None,
+                                     None, 0) == _lib.HIP_ERROR_INVALID_VALUE

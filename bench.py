@@ -187,9 +187,10 @@ def tile_phases(torch, ex, runs: int = 3) -> dict:
     work table): the mean cycles from its start until one wave's first-stage loads have landed
     (first_stage), until every wave has them (k_loop_start), the k-loop per k-stage (summed cycles
     over summed stages), the hand-over of the next index, the epilogue until its last wave is done,
-    and next_start: from the last epilogue wave's end to the same workgroup's next tile start
-    (negative where its first waves start the next tile while the slowest still stores).  The
-    median launch of `runs`."""
+    next_start: from the last epilogue wave's end to the same workgroup's next tile start
+    (negative where its first waves start the next tile while the slowest still stores), and
+    middle_step: the per-wave parts of the k-loop step k = stages / 2.  The median launch of
+    `runs`."""
     import numpy as np
 
     from grouped_gemm_gpu_kernel_amd import _lib
@@ -235,11 +236,27 @@ def tile_phases(torch, ex, runs: int = 3) -> dict:
         "all": np.ones(len(ph), bool),
     }
     out = {"work_tiles": int(len(ph)), "work_tile_rows": bm, "work_tile_cols": bn}
+    # The middle k-loop step of each tile, per wave: issuing the next stage's loads, issuing the
+    # MFMAs and fragment reads, the wait for the loads, the closing barrier (mean over the waves),
+    # and the step from the first wave's start to the last wave's barrier.
+    step = ph[:, _lib.GGK_PHASE_STEP:].reshape(len(ph), _lib.GGK_PHASE_STEP_WAVES,
+                                                _lib.GGK_PHASE_STEP_MARKS).astype(np.float64)
+    stamped = (step[:, :, 0] > 0)
     for name, sel in classes.items():
         if not sel.any():
             continue
         g = gap[sel]
         g = g[~np.isnan(g)]
+        st = sel & stamped.any(axis=1)
+        step_row = None
+        if st.any():
+            w = stamped[st]
+            parts = [np.where(w, step[st, :, i + 1] - step[st, :, i], np.nan) for i in range(4)]
+            span = (np.where(w, step[st, :, 4], -np.inf).max(axis=1) - np.where(w, step[st, :, 0], np.inf).min(axis=1))
+            step_row = {"issue": round(float(np.nanmean(parts[0]))), "mfma": round(float(np.nanmean(parts[1]))),
+                        "wait": round(float(np.nanmean(parts[2]))), "barrier": round(float(np.nanmean(parts[3]))),
+                        "barrier_max_wave": round(float(np.nanmean(np.nanmax(parts[3], axis=1)))),
+                        "step": round(float(span.mean()))}
         out[name] = {
             "tiles": int(sel.sum()), "stages": round(float(stages[sel].mean()), 2),
             "first_stage": round(float((first - start)[sel].mean())),
@@ -248,6 +265,7 @@ def tile_phases(torch, ex, runs: int = 3) -> dict:
             "hand_over": round(float((epi - ke)[sel].mean())),
             "epilogue": round(float((epi_end - epi)[sel].mean())),
             "next_start": round(float(g.mean())) if g.size else None,
+            "middle_step": step_row,
         }
     tile = (epi_end - start).sum()
     out["share"] = {"to_k_loop": round(float((kl - start).sum() / tile), 4),

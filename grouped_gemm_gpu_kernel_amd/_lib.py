@@ -38,7 +38,8 @@ GGK_SCHEDULER_STATE_INTS = GGK_SCHEDULER_COUNTER_STRIDE * (GGK_SCHEDULER_CHUNKS 
 GGK_WORK_HALF_SHIFT = 28  # work-table entry: local work tile | (1: first, 2: second half of rows) << shift
 GGK_PHASE_WALL, GGK_PHASE_START, GGK_PHASE_FIRST_STAGE, GGK_PHASE_K_LOOP = 0, 1, 2, 3
 GGK_PHASE_K_END, GGK_PHASE_EPILOGUE, GGK_PHASE_EPILOGUE_END, GGK_PHASE_WHO = 4, 5, 6, 7
-GGK_PHASE_COUNT = 8
+GGK_PHASE_STEP, GGK_PHASE_STEP_MARKS, GGK_PHASE_STEP_WAVES = 8, 5, 8
+GGK_PHASE_COUNT = 48
 GGK_MOE_MAX_EXPERTS = 1024
 GGK_MOE_HEADER_INTS = 16
 GGK_MOE_STATUS = 12

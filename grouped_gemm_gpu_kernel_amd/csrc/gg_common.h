@@ -211,6 +211,7 @@ template <int V> struct KernelShape<V, GGK_PATH_FMA> {
 // compiles to nothing.
 struct NoStamps {
   __device__ __forceinline__ void mark(int) const {}
+  __device__ __forceinline__ void step_mark(int) const {}
   __device__ __forceinline__ void wave_done() const {}
 };
 struct PhaseStamps {
@@ -218,6 +219,13 @@ struct PhaseStamps {
   __device__ __forceinline__ void mark(int i) const {
     if (slot != nullptr && __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) == 0) {
       slot[i] = static_cast<long long>(__builtin_amdgcn_s_memtime());
+    }
+  }
+  // Every wave (lane 0): mark i of the k-loop step that is stamped (GGK_PHASE_STEP).
+  __device__ __forceinline__ void step_mark(int i) const {
+    if (slot != nullptr && (threadIdx.x & (kWave - 1)) == 0) {
+      const int wave = threadIdx.x / kWave;
+      slot[GGK_PHASE_STEP + GGK_PHASE_STEP_MARKS * wave + i] = static_cast<long long>(__builtin_amdgcn_s_memtime());
     }
   }
   // Every wave, when its epilogue has been issued.

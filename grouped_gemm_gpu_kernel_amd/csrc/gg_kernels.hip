@@ -317,6 +317,7 @@ __global__ GG_KERNEL_ATTRS(V, PATH) void gg_grouped_kernel(GroupedArgs args) {
       handed = true;
     };
     // Phase stamps of this work tile (traced launches with a phase buffer only).
+    static_assert(G::THREADS <= kWave * GGK_PHASE_STEP_WAVES, "one step-stamp row per wave");
     PhaseStamps stamps{TRACED && args.tile_phases != nullptr ? args.tile_phases + (long long)GGK_PHASE_COUNT * t
                                                              : nullptr};
     auto after_k_loop = [&]() {

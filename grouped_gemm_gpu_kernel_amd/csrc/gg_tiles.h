@@ -106,16 +106,22 @@ __device__ __forceinline__ void run_k_loop_dma(const gg_device_problem_desc& p, 
   for (int k = 0; k < nk; ++k) {
     const int ul = u == 0 ? L : u - 1;  // (u + L) % NBUF
     const int un = u == NBUF - 1 ? 0 : u + 1;
+    const bool stamped = k == nk / 2;  // the step whose timing a traced launch records
+    if (stamped) stamps.step_mark(0);
     loader.issue(k + L, lds + ul * G::STAGE);
     const bool extra = k == 0 && __builtin_amdgcn_readfirstlane(on_start() ? 1 : 0) != 0;
+    if (stamped) stamps.step_mark(1);
     compute(lds + u * G::STAGE);
+    if (stamped) stamps.step_mark(2);
     if (extra) {
       wait_vmcnt<PENDING + 1>();
     } else {
       wait_vmcnt<PENDING>();
     }
+    if (stamped) stamps.step_mark(3);
     if (k + 1 == loader.last_stage) loader.fix_last_stage(k + 1, lds + un * G::STAGE);
     stage_barrier();
+    if (stamped) stamps.step_mark(4);
     u = un;
   }
 }

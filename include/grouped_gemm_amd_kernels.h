@@ -253,7 +253,14 @@ enum {
   GGK_PHASE_WHO = 7,          /* workgroup | half << 20 (0 whole, 1 / 2 a row half) | rows << 22 |
                                  cols << 34 | stages << 46: the tile's rows and columns inside its
                                  problem (at most the work tile's), its k-stages */
-  GGK_PHASE_COUNT = 8
+  /* Entry GGK_PHASE_STEP + GGK_PHASE_STEP_MARKS w + i: wave w's core clock in the k-loop step
+   * k = stages / 2 (LDS-DMA k-loops only; zero elsewhere): i = 0 the step starts, 1 its loads of
+   * the next stage are issued, 2 its MFMAs and fragment reads are issued, 3 its loads have landed
+   * (the step's vmcnt wait is over), 4 the step's closing barrier is passed. */
+  GGK_PHASE_STEP = 8,
+  GGK_PHASE_STEP_MARKS = 5,
+  GGK_PHASE_STEP_WAVES = 8,   /* waves per workgroup at most */
+  GGK_PHASE_COUNT = 48        /* GGK_PHASE_STEP + GGK_PHASE_STEP_MARKS GGK_PHASE_STEP_WAVES */
 };
 hipError_t ggk_launch_grouped_traced(int variant, int path, int addressing,
                                      const gg_device_problem_desc* d_problems, const int* d_tile_offsets,

@@ -894,7 +894,8 @@ def test_wall_clock_trace(torch):
 def test_tile_phase_stamps(torch, name):
     """A traced launch with a phase buffer computes the same D bits as run() and stamps every
     launched work tile once, its phases in order (start <= first stage <= k-loop <= k-loop end <=
-    epilogue <= last epilogue end), by a workgroup of the grid."""
+    epilogue <= last epilogue end), by a workgroup of the grid, and each of its waves' five marks of
+    the middle k-loop step in order within the k-loop."""
     spec = make_spec(name)
     dw = DeviceWorkload(spec)
     cfg = KernelConfig.named("128x64x32")
@@ -919,6 +920,20 @@ def test_tile_phase_stamps(torch, name):
         assert (ph[:, a] <= ph[:, b]).all(), (a, b)
     wg = ph[:, _lib.GGK_PHASE_WHO] & 0xFFFFF
     assert ((wg >= 0) & (wg < ex.grid_ctas())).all()
+    # Every wave stamps the middle k-loop step of every tile with stages, in order, inside the
+    # tile's k-loop (one CU's core clock); the waves a tile's kernel does not have stay zero.
+    shape, _, _, _ = ex.schedule()
+    waves = shape.threads // 64
+    stages = (ph[:, _lib.GGK_PHASE_WHO] >> 46) & 0x1FFFF
+    step = ph[:, _lib.GGK_PHASE_STEP:].reshape(n, _lib.GGK_PHASE_STEP_WAVES, _lib.GGK_PHASE_STEP_MARKS)
+    live = stages > 0
+    assert live.any()
+    assert (step[live, :waves, :] > 0).all(), "a wave did not stamp its middle step"
+    assert (step[:, waves:, :] == 0).all() and (step[~live] == 0).all()
+    for i in range(_lib.GGK_PHASE_STEP_MARKS - 1):
+        assert (step[live, :waves, i] <= step[live, :waves, i + 1]).all(), i
+    assert (step[live, :waves, 0] >= ph[live, _lib.GGK_PHASE_K_LOOP, None]).all()
+    assert (step[live, :waves, 4] <= ph[live, _lib.GGK_PHASE_K_END, None]).all()
     say(f"{name}: {n} work tiles stamped, mean k-loop share "
         f"{float(np.mean((ph[:, 4] - ph[:, 3]) / np.maximum(ph[:, 6] - ph[:, 1], 1))):.3f}")
     ex.close()

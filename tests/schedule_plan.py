@@ -1,7 +1,9 @@
-"""The executor's work-tile schedule, restated for the tests (not collected: no test_ prefix).
+"""The executor's work-tile schedule and launch plan, restated for the tests (not collected: no
+test_ prefix).
 
-plan_schedule in csrc/grouped_gemm.cpp plans it on the host; moe_prepare_kernel in csrc/gg_moe.hip
-plans the same one on the device.  It is this library's own load-balancing heuristic (the
+plan_schedule in csrc/grouped_gemm.cpp plans the schedule on the host; moe_prepare_kernel in
+csrc/gg_moe.hip plans the same one on the device.  plan_launch (csrc/grouped_gemm.cpp) adds the
+variant choice, the grid and the work table with its tail halves.  It is this library's own load-balancing heuristic (the
 reference claims tiles from one counter in tile order), so it has no reference counterpart; D does
 not depend on it."""
 import heapq

@@ -3,9 +3,9 @@ test_ prefix).
 
 plan_schedule in csrc/grouped_gemm.cpp plans the schedule on the host; moe_prepare_kernel in
 csrc/gg_moe.hip plans the same one on the device.  plan_launch (csrc/grouped_gemm.cpp) adds the
-variant choice, the grid and the work table with its tail halves.  It is this library's own load-balancing heuristic (the
-reference claims tiles from one counter in tile order), so it has no reference counterpart; D does
-not depend on it."""
+variant choice, the grid and the work table with its tail halves.  All of it is this library's
+own load balancing (the reference claims tiles from one counter in tile order), so it has no
+reference counterpart; D does not depend on it."""
 import heapq
 import math
 

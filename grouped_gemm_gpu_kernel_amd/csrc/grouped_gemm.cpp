@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <array>
+#include <climits>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -40,7 +41,11 @@ constexpr int kRegAllocGranule = 8;
 constexpr int kMaxWavesPerSimd = 8;
 constexpr int kSimdsPerCu = 4;
 
-int ceil_div(int x, int y) { return (x + y - 1) / y; }
+// ceil(x / y) for x >= 0, y > 0, without forming x + y - 1 (which overflows near INT_MAX).
+int ceil_div(int x, int y) { return x / y + (x % y != 0 ? 1 : 0); }
+
+// a + b for non-negative ints, saturating at INT_MAX.
+int add_saturating(int a, int b) { return a > INT_MAX - b ? INT_MAX : a + b; }
 
 // The three accepted shapes (resolve_variant, src/grouped_gemm.cu:67-81).
 int resolve_variant(const KernelConfig& config) {
@@ -459,9 +464,12 @@ int grid_ctas_for(int total_tiles, const KernelConfig& config, const OccupancyIn
   return std::max(1, grid);
 }
 
+// Clamped at INT_MAX: a problem (or set) of more tiles than an int holds gets tile offsets that do
+// not match its tile count, which build() rejects.
 int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& config) {
   if (problem.m <= 0 || problem.n <= 0 || config.cta_m <= 0 || config.cta_n <= 0) return 0;
-  return ceil_div(problem.m, config.cta_m) * ceil_div(problem.n, config.cta_n);
+  const int64_t tiles = static_cast<int64_t>(ceil_div(problem.m, config.cta_m)) * ceil_div(problem.n, config.cta_n);
+  return tiles > INT_MAX ? INT_MAX : static_cast<int>(tiles);
 }
 
 DeviceProblemDesc to_device_problem(const ProblemDesc& p, const KernelConfig& config) {
@@ -538,7 +546,7 @@ PreparedProblemSet prepare_problem_set(const std::vector<ProblemDesc>& problems,
   prepared.tile_offsets.reserve(count + 1);
   for (int idx : prepared.sorted_to_original) {
     prepared.sorted_problems.push_back(problems[idx]);
-    prepared.tile_offsets.push_back(prepared.tile_offsets.back() + keys[idx].tiles);
+    prepared.tile_offsets.push_back(add_saturating(prepared.tile_offsets.back(), keys[idx].tiles));
   }
   prepared.total_tiles = prepared.tile_offsets.back();
   return prepared;
@@ -673,12 +681,15 @@ hipError_t plan_launch(const std::vector<DeviceProblemDesc>& problems, const Ker
   const int base_variant = resolve_variant(config);
   if (base_variant < 0 || compute_units < 1 || !blocks_per_cu) return hipErrorInvalidValue;
   const int count = static_cast<int>(problems.size());
+  int64_t tiles = 0;  // the set's macro-tiles: the work-tile counts below stay under it
   for (const DeviceProblemDesc& p : problems) {
     if (p.m < 0 || p.n < 0 || p.k < 0) return hipErrorInvalidValue;
     const bool live = p.m > 0 && p.n > 0;
     if (p.tiles_m != (live ? ceil_div(p.m, config.cta_m) : 0) || p.tiles_n != (live ? ceil_div(p.n, config.cta_n) : 0)) {
       return hipErrorInvalidValue;
     }
+    tiles += static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+    if (tiles > INT_MAX) return hipErrorInvalidValue;
   }
   int variant = base_variant;
   const int path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;

@@ -200,7 +200,9 @@ int count_non_empty_problems(
 // src/grouped_gemm.cu:912-930
 DeviceProblemDesc to_device_problem(const ProblemDesc& problem, const KernelConfig& config);
 
-// src/grouped_gemm.cu:54-65
+// src/grouped_gemm.cu:54-65.  Clamped at INT_MAX (the reference's int product
+// overflows); prepare_problem_set's offsets saturate there too, and build()
+// rejects such a set (its offsets no longer step by the tile counts).
 int tile_count_for_problem(const ProblemDesc& problem, const KernelConfig& config);
 
 // Persistent grid size build() chooses (src/grouped_gemm.cu:1228-1236):
@@ -245,8 +247,9 @@ struct LaunchPlan {
 using BlocksPerCu = std::function<hipError_t(int variant, int path, int* blocks)>;
 
 // hipErrorInvalidValue for a configuration without a kernel, compute_units
-// below 1, a negative extent or tile counts that are not the ceilings of
-// m / cta_m and n / cta_n (zero for an empty problem).
+// below 1, a negative extent, tile counts that are not the ceilings of
+// m / cta_m and n / cta_n (zero for an empty problem), or a set of more than
+// INT_MAX macro-tiles.
 hipError_t plan_launch(const std::vector<DeviceProblemDesc>& problems, const KernelConfig& config,
                        int compute_units, const BlocksPerCu& blocks_per_cu, LaunchPlan* plan);
 

@@ -248,3 +248,27 @@ def test_launch_plan_rejects_bad_input():
     assert plan.table_ints == 2 and plan.grid == 256
     assert _lib.lib().gg_plan_launch(arr, 1, ctypes.byref(cfg.to_c()), 256, None, ctypes.byref(plan), None, None,
                                      None, 0) == _lib.HIP_ERROR_INVALID_VALUE
+
+
+def test_extreme_extents_stay_defined():
+    """Tile counts of extents near INT_MAX: ceil(m / cta_m) without overflow (the sanitized run of
+    this file checks it), a product past INT_MAX clamped there, prepare's offsets saturating at it,
+    and the launch plan refusing a set of more than INT_MAX macro-tiles.  The reference's int
+    arithmetic overflows there (src/grouped_gemm.cu:54-65)."""
+    from grouped_gemm_gpu_kernel_amd import _lib
+    big = 2**31 - 1
+    cfg = KernelConfig.named("128x64x32")
+    tall = ProblemDesc(big, 1, 1, 1, 1, None, 1, 1, 1, 1, 1)
+    assert api.tile_count_for_problem(tall, cfg) == -(-big // 128)
+    huge = ProblemDesc(big, big, 1, 1, 1, None, 1, 1, big, big, big)
+    assert api.tile_count_for_problem(huge, cfg) == big
+    prep = api.prepare_problem_set([tall, huge, tall], cfg, SortMode.kNone)
+    assert prep.tile_offsets == [0, -(-big // 128), big, big] and prep.total_tiles == big
+    plan = api.plan_launch([tall], cfg, 256, [1, 1, 1, 2, 2, 2])
+    assert plan.total_work == -(-(-(-big // 128)) // 2) and plan.work_table == []  # above 2^22: searched
+    with pytest.raises(_lib.HipError):
+        api.plan_launch([huge], cfg, 256, [1, 1, 1, 2, 2, 2])
+    with pytest.raises(_lib.HipError):
+        # 2^30 macro-tiles each: the set's 2^31 no longer fits an int
+        api.plan_launch([ProblemDesc(2**30, 2**13, 1, 1, 1, None, 1, 1, 2**13, 2**13, 2**13)] * 2, cfg, 256,
+                        [1, 1, 1, 2, 2, 2])

@@ -52,6 +52,9 @@ def parse_args():
                     help="only run a plain device-to-device copy of MIB MiB a few times (for scaling HBM "
                          "byte counters of a profiler run) and exit")
     ap.add_argument("--no-moe-device", action="store_true", help="skip the device-side MoE prepare timing")
+    ap.add_argument("--shards", default="", metavar="N[,N...]",
+                    help="also time each rank's share of N-way data-parallel splits (plan_shards), every "
+                         "share run on this GPU, as the 'shards' list of the JSON line")
     ap.add_argument("--phases", action="store_true",
                     help="also report per-work-tile phase cycles of each mode (traced launches with phase stamps)")
     ap.add_argument("--profile-summary", nargs="+", metavar="DIR",
@@ -273,6 +276,45 @@ def tile_phases(torch, ex, runs: int = 3) -> dict:
                     "hand_over": round(float((epi - ke).sum() / tile), 4),
                     "epilogue": round(float((epi_end - epi).sum() / tile), 4)}
     return out
+
+
+def shard_shares(torch, probs, cfg, mode, ranks: int, stream, steps: int, warmup: int, warm_seconds: float,
+                 whole_ms: float, flops: float) -> dict:
+    """One GPU's share of an N-way data-parallel split, for every rank: plan_shards splits the set
+    (whole problems; column ranges of the ones above a rank's share), and each rank's share is built
+    and timed on this GPU as the rank would run it on its own.  The N shares of a step would run
+    side by side, so the slowest one sets the step: balance = mean / max share time, and
+    whole_over_max = the unsplit set's time on one GPU over the slowest share's.  Nothing is
+    exchanged between ranks (problems are independent), so no collective is timed."""
+    from grouped_gemm_gpu_kernel_amd import api
+
+    pieces = api.plan_shards(probs, cfg, ranks)
+    shares, executors = [], []
+    for r in range(ranks):
+        share = [api.shard_problem(probs[p.problem], p) for p in pieces if p.rank == r]
+        ex = api.GroupedGemmExecutor()
+        st = ex.build(api.prepare_problem_set(share, cfg, mode), cfg)
+        if st != 0:
+            raise RuntimeError(f"rank {r} build: hipError_t {st}")
+        shares.append(share)
+        executors.append(ex)
+    # Two passes over the ranks, the faster time of each: the first share timed after the set's
+    # own runs otherwise reads slow now and then.
+    best_ms = [math.inf] * ranks
+    for _ in range(2):
+        for r, ex in enumerate(executors):
+            warm_clock(torch, lambda: ex.run(stream), warm_seconds)
+            best_ms[r] = min(best_ms[r], time_runs(torch, lambda: ex.run(stream), steps, warmup))
+    for ex in executors:
+        ex.close()
+    rank_ms = [round(ms, 4) for ms in best_ms]
+    rank_tflops = [round(api.total_flops(share) / (ms * 1e-3) / 1e12, 2) for share, ms in zip(shares, best_ms)]
+    slowest = max(rank_ms)
+    return {"ranks": ranks, "pieces": len(pieces), "split_problems": len(pieces) - len({p.problem for p in pieces}),
+            "rank_ms": rank_ms, "rank_tflops": rank_tflops, "max_ms": slowest,
+            "balance": round(sum(rank_ms) / (ranks * slowest), 4), "whole_ms": round(whole_ms, 4),
+            "whole_over_max": round(whole_ms / slowest, 3),
+            "aggregate_tflops_at_max": round(flops / (slowest * 1e-3) / 1e12, 2)}
 
 
 def torch_binding(torch, dw, cfg, mode, stream, steps: int, warmup: int, warm_seconds: float) -> dict:
@@ -730,6 +772,13 @@ def main() -> int:
     torch_op = None if args.no_torch_op else torch_binding(torch, dw, cfg, best_mode, stream, args.steps,
                                                           args.warmup, warm_s)
     cpu = None if args.no_cpu else cpu_baseline(dw, spec, args.cpu_seconds, args.cpu_full)
+    shards = None
+    if args.shards:
+        shards = []
+        for ranks in (int(x) for x in args.shards.split(",")):
+            shards.append(shard_shares(torch, probs, cfg, best_mode, ranks, stream, args.steps, args.warmup,
+                                       warm_s, best[1], flops))
+            print(f"# shards {shards[-1]}", file=sys.stderr, flush=True)
 
     row, ms = best
     tflops = flops / (ms * 1e-3) / 1e12
@@ -782,6 +831,8 @@ def main() -> int:
         "vendor_hipblaslt": vendor_rows,
         "moe_device_prepare": moe_device,
     }
+    if shards is not None:
+        out["shards"] = shards
     if args.table:
         print(f"{'mode':24}{'prep_ms':>10}{'kernel_ms':>11}{'tflops':>10}{'tiles':>8}{'grid':>7}{'launches':>10}"
               f"{'tail_share':>12}", file=sys.stderr)

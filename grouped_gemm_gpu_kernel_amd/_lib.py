@@ -117,6 +117,11 @@ class GGLaunchPlan(ctypes.Structure):
     ]
 
 
+class GGShardPiece(ctypes.Structure):
+    """gg_shard_piece (grouped_gemm_amd.h)"""
+    _fields_ = [("problem", ctypes.c_int), ("rank", ctypes.c_int), ("col0", ctypes.c_int), ("cols", ctypes.c_int)]
+
+
 class GGKMoeLayout(ctypes.Structure):
     """ggk_moe_layout (grouped_gemm_amd_kernels.h)"""
     _fields_ = [
@@ -158,6 +163,7 @@ SIGNATURES = {
     "gg_run_baseline_per_problem": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _vp]),
     "gg_count_non_empty_problems": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig)]),
     "gg_grid_ctas_for": (_i, [_P(GGKernelConfig), _i]),
+    "gg_plan_shards": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _i, _P(GGShardPiece), _i]),
     "gg_plan_launch": (_i, [_P(GGProblemDesc), _i, _P(GGKernelConfig), _i, c_int_p, _P(GGLaunchPlan), c_int_p,
                             c_int_p, c_int_p, _i]),
     "gg_moe_create": (_i, [_P(GGKMoeLayout), _P(GGKernelConfig), _i, _P(_vp)]),

@@ -377,6 +377,38 @@ def plan_launch(sorted_problems: Sequence[ProblemDesc], config: KernelConfig, co
                       list(plan.launch_bounds))
 
 
+@dataclass
+class ShardPiece:
+    """One piece of a data-parallel split (no reference counterpart): columns [col0, col0 + cols) of
+    problem `problem`, computed by rank `rank`."""
+    problem: int
+    rank: int
+    col0: int
+    cols: int
+
+
+def plan_shards(problems: Sequence[ProblemDesc], config: KernelConfig, ranks: int) -> list:
+    """A split of the problems across `ranks` GPUs (grouped_gemm::plan_shards): a list of ShardPiece
+    in problem and column order.  Host only."""
+    count = len(problems)
+    arr = _problem_array(problems)
+    cap = count + ranks
+    out = (_lib.GGShardPiece * max(1, cap))()
+    got = _lib.lib().gg_plan_shards(arr, count, ctypes.byref(config.to_c()), ranks, out, cap)
+    if got < 0:
+        raise _lib.HipError(-got, "gg_plan_shards")
+    return [ShardPiece(p.problem, p.rank, p.col0, p.cols) for p in out[:got]]
+
+
+def shard_problem(problem: ProblemDesc, piece: ShardPiece) -> ProblemDesc:
+    """The problem a piece computes: the same A, B, C and D from column col0 on, n = cols
+    (grouped_gemm::shard_problem)."""
+    from dataclasses import replace
+    return replace(problem, n=piece.cols, b=(problem.b + 2 * piece.col0) if problem.b else problem.b,
+                   c=(problem.c + 4 * piece.col0) if problem.c else problem.c,
+                   d=(problem.d + 4 * piece.col0) if problem.d else problem.d)
+
+
 def total_flops(problems: Sequence[ProblemDesc]) -> float:
     """sum of 2*m*n*k (bench/benchmark_grouped_gemm.cu:570-576)."""
     return float(sum(2.0 * p.m * p.n * p.k for p in problems))

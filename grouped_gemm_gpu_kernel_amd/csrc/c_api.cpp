@@ -333,6 +333,25 @@ int gg_plan_launch(const gg_problem_desc* sorted_problems, int count, const gg_k
   }
 }
 
+int gg_plan_shards(const gg_problem_desc* problems, int count, const gg_kernel_config* config, int ranks,
+                   gg_shard_piece* pieces, int capacity) {
+  if (config == nullptr || bad_list(problems, count) || (capacity > 0 && pieces == nullptr)) {
+    return -static_cast<int>(hipErrorInvalidValue);
+  }
+  try {
+    std::vector<gg::ShardPiece> out;
+    const hipError_t status = gg::plan_shards(to_cpp(problems, count), to_cpp(*config), ranks, &out);
+    if (status != hipSuccess) return -static_cast<int>(status);
+    if (static_cast<int>(out.size()) > capacity) return -static_cast<int>(hipErrorInvalidValue);
+    for (size_t i = 0; i < out.size(); ++i) {
+      pieces[i] = gg_shard_piece{out[i].problem, out[i].rank, out[i].col0, out[i].cols};
+    }
+    return static_cast<int>(out.size());
+  } catch (...) {
+    return -static_cast<int>(hipErrorOutOfMemory);
+  }
+}
+
 int gg_moe_create(const ggk_moe_layout* layout, const gg_kernel_config* config, int sort_mode, gg_moe** out) {
   if (out == nullptr) return hipErrorInvalidValue;
   *out = nullptr;

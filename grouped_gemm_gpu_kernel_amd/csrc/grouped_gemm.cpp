@@ -1028,6 +1028,81 @@ int count_non_empty_problems(const std::vector<ProblemDesc>& problems, const Ker
   return count;
 }
 
+// The problems are independent, so a split across GPUs needs no exchange: each piece (a whole
+// problem or a range of its columns) goes to one rank.  Pieces are cut at work-tile column
+// boundaries, so every element of D is computed by the same work tile, with the same k order, as
+// in the unsplit set.
+hipError_t plan_shards(const std::vector<ProblemDesc>& problems, const KernelConfig& config, int ranks,
+                       std::vector<ShardPiece>* pieces) {
+  if (pieces == nullptr) return hipErrorInvalidValue;
+  pieces->clear();
+  const int variant = resolve_variant(config);
+  if (variant < 0 || ranks < 1) return hipErrorInvalidValue;
+  const int path = config.use_tensor_cores ? GGK_PATH_MFMA : GGK_PATH_FMA;
+  ggk_work_shape shape{};
+  const hipError_t status = ggk_work_shape_get(variant, path, &shape);
+  if (status != hipSuccess) return status;
+  const int bm = config.cta_m * shape.tiles_m;
+  const int bn = config.cta_n * shape.tiles_n;
+  // Estimated time of columns [col0, col0 + cols) of problem p (the schedule's tile-time model).
+  auto estimate = [&](const ProblemDesc& p, int cols) {
+    if (p.m <= 0 || cols <= 0) return 0.0;
+    const bool reads_c = p.c != nullptr && p.beta != 0.0f;
+    return problem_work_time(p.m, cols, p.k, ceil_div(p.m, bm), ceil_div(cols, bn), shape.stage_k, reads_c);
+  };
+  double total = 0.0;
+  for (const ProblemDesc& p : problems) {
+    if (p.m < 0 || p.n < 0 || p.k < 0) return hipErrorInvalidValue;
+    total += estimate(p, p.n);
+  }
+  const double share = total / ranks;
+  std::vector<ShardPiece> out;
+  std::vector<double> time;
+  for (int i = 0; i < static_cast<int>(problems.size()); ++i) {
+    const ProblemDesc& p = problems[i];
+    const double t = estimate(p, p.n);
+    const int wtn = p.n > 0 ? ceil_div(p.n, bn) : 0;
+    // A problem above one rank's share is cut into that many column ranges (at most one per
+    // work-tile column), as even as whole work-tile columns allow.
+    int parts = 1;
+    if (share > 0.0 && t > share && wtn > 1) {
+      parts = static_cast<int>(std::min<double>(wtn, std::ceil(t / share)));
+    }
+    int first = 0;
+    for (int part = 0; part < parts; ++part) {
+      const int span = wtn / parts + (part < wtn % parts ? 1 : 0);
+      const int col0 = first * bn;
+      const int cols = parts == 1 ? p.n : std::min(p.n - col0, span * bn);
+      out.push_back(ShardPiece{i, 0, col0, cols});
+      time.push_back(parts == 1 ? t : estimate(p, cols));
+      first += span;
+    }
+  }
+  // Longest piece first (stable), each to the rank with the least estimated time so far (ties:
+  // the lowest rank).
+  std::vector<int> by_time(out.size());
+  std::iota(by_time.begin(), by_time.end(), 0);
+  std::stable_sort(by_time.begin(), by_time.end(), [&](int x, int y) { return time[x] > time[y]; });
+  std::vector<double> load(ranks, 0.0);
+  for (const int j : by_time) {
+    if (time[j] <= 0.0) continue;  // an empty problem: rank 0
+    const int r = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    out[j].rank = r;
+    load[r] += time[j];
+  }
+  *pieces = std::move(out);
+  return hipSuccess;
+}
+
+ProblemDesc shard_problem(const ProblemDesc& problem, const ShardPiece& piece) {
+  ProblemDesc out = problem;
+  out.n = piece.cols;
+  out.b = problem.b != nullptr ? problem.b + piece.col0 : nullptr;
+  out.c = problem.c != nullptr ? problem.c + piece.col0 : nullptr;
+  out.d = problem.d != nullptr ? problem.d + piece.col0 : nullptr;
+  return out;
+}
+
 // ---------------------------------------------------------------------------
 // MoeGroupedGemm: device-side prepare + grouped launch (no reference counterpart).
 

@@ -253,6 +253,29 @@ using BlocksPerCu = std::function<hipError_t(int variant, int path, int* blocks)
 hipError_t plan_launch(const std::vector<DeviceProblemDesc>& problems, const KernelConfig& config,
                        int compute_units, const BlocksPerCu& blocks_per_cu, LaunchPlan* plan);
 
+// Addition with no counterpart in the reference: a data-parallel split of a
+// problem list across `ranks` GPUs.  Problems are independent, so no data
+// moves between ranks.  Each piece is a whole problem or, for a problem whose
+// estimated time exceeds one rank's share (the total over `ranks`), one of
+// several ranges of its columns cut at work-tile column boundaries, so D comes
+// out bit for bit as in the unsplit set.  The estimate is the executor's
+// schedule model on the configuration's own work tile.  Pieces go longest
+// first, each to the rank with the least estimated time so far (ties: the
+// lowest rank).  `pieces` lists them in problem order and column order.
+// Empty problems stay whole (on rank 0).  At most problems.size() + ranks
+// pieces result.  hipErrorInvalidValue for a configuration without a kernel,
+// ranks below 1 or a negative extent.
+struct ShardPiece {
+  int problem;  // index into the problem list
+  int rank;     // 0 .. ranks - 1
+  int col0;     // first column of D (and of B and C) the piece covers
+  int cols;     // columns covered
+};
+hipError_t plan_shards(const std::vector<ProblemDesc>& problems, const KernelConfig& config, int ranks,
+                       std::vector<ShardPiece>* pieces);
+// The problem a piece computes: columns [col0, col0 + cols) of `problem`.
+ProblemDesc shard_problem(const ProblemDesc& problem, const ShardPiece& piece);
+
 // ---------------------------------------------------------------------------
 // Additions with no counterpart in the reference: the grouped GEMM of a
 // mixture-of-experts layer, prepared on the device from device-side token

@@ -173,6 +173,20 @@ int gg_plan_launch(const gg_problem_desc* sorted_problems, int count, const gg_k
                    int compute_units, const int* blocks_per_cu, gg_launch_plan* plan, int* order,
                    int* work_offsets, int* table, int table_capacity);
 
+/* grouped_gemm::plan_shards (no reference counterpart): a data-parallel split
+ * of count problems across `ranks` GPUs, see grouped_gemm.h.  Writes the
+ * pieces, in problem order, to pieces[capacity] and returns their number (at
+ * most count + ranks), or a negative hipError_t; fewer than that many slots:
+ * -hipErrorInvalidValue. */
+typedef struct gg_shard_piece {
+  int problem;
+  int rank;
+  int col0;
+  int cols;
+} gg_shard_piece;
+int gg_plan_shards(const gg_problem_desc* problems, int count, const gg_kernel_config* config, int ranks,
+                   gg_shard_piece* pieces, int capacity);
+
 /* MoeGroupedGemm (no reference counterpart): a mixture-of-experts group whose
  * problem set is prepared on the device from device-side token counts, see
  * ggk_moe_prepare for the layout.  gg_moe_create checks the layout and

@@ -198,3 +198,49 @@ def plan_launch(problems, cta, mfma, compute_units, blocks_per_cu, work_shape, h
     return dict(variant=variant, addressing=addressing, total_work=total_work,
                 launch_total=len(table) // 2 if table else total_work, grid=grid, halves=halves, order=order,
                 offsets=offsets, bounds=bounds, table=table, launch_bounds=launch)
+
+
+def plan_shards(problems, ranks, bm, bn, bk):
+    """grouped_gemm::plan_shards (csrc/grouped_gemm.cpp) for problems (m, n, k, reads_c): the
+    estimate of a piece of `cols` columns is the schedule's model on bm x bn work tiles (unclamped
+    double); a problem above one rank's share (total / ranks) is cut into min(work-tile columns,
+    ceil(t / share)) column ranges, the first ones one work-tile column wider when they do not divide
+    evenly; pieces go longest first (stable), each to the least-loaded rank (lowest on ties), an
+    empty problem whole to rank 0.  Returns [(problem, rank, col0, cols)] in problem order."""
+    def estimate(m, cols, k, reads_c):
+        if m <= 0 or cols <= 0:
+            return 0.0
+        tm, tn = (m - 1) // bm + 1, (cols - 1) // bn + 1
+        wt = float(tm) * tn
+        stages = float((k - 1) // bk + 1) if k > 0 else 0.0
+        edge = float(m) * tn + float(cols) * tm
+        stage = 310000.0 * wt + 290.0 * edge
+        return 1500000.0 * wt + stages * stage + (46.0 if reads_c else 23.0) * (float(m) * cols)
+
+    total = 0.0
+    for (m, n, k, c) in problems:
+        total += estimate(m, n, k, c)
+    share = total / ranks
+    pieces, times = [], []
+    for i, (m, n, k, c) in enumerate(problems):
+        t = estimate(m, n, k, c)
+        wtn = (n - 1) // bn + 1 if n > 0 else 0
+        parts = 1
+        if share > 0.0 and t > share and wtn > 1:
+            parts = int(min(float(wtn), math.ceil(t / share)))
+        first = 0
+        for part in range(parts):
+            span = wtn // parts + (1 if part < wtn % parts else 0)
+            col0 = first * bn
+            cols = n if parts == 1 else min(n - col0, span * bn)
+            pieces.append([i, 0, col0, cols])
+            times.append(t if parts == 1 else estimate(m, cols, k, c))
+            first += span
+    load = [0.0] * ranks
+    for j in sorted(range(len(pieces)), key=lambda j: -times[j]):
+        if times[j] <= 0.0:
+            continue
+        r = min(range(ranks), key=lambda x: load[x])
+        pieces[j][1] = r
+        load[r] += times[j]
+    return [tuple(p) for p in pieces]

@@ -949,3 +949,28 @@ def test_cpp_dropin_driver(torch):
     sys.stdout.write(out.stdout[-4000:])
     assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-2000:]
     assert "All correctness checks passed." in out.stdout
+
+
+@pytest.mark.parametrize("name,ranks", [("moe64", 8), ("mixed512", 3)])
+def test_shards_give_the_unsplit_d(torch, name, ranks):
+    """A data-parallel split (plan_shards: whole problems, and column ranges of the ones above a
+    rank's share) run rank by rank on this GPU writes the same D bits as the unsplit set: each
+    element is computed by the same work tile with the same k order."""
+    spec = make_spec(name)
+    dw = DeviceWorkload(spec)
+    probs = dw.problems()
+    cfg = KernelConfig.named(spec.config)
+    dw.poison_d()
+    assert api.run_grouped_gemm_once(probs, SortMode.kByTiles, cfg) == 0
+    torch.cuda.synchronize()
+    want = dw.d.clone()
+    pieces = api.plan_shards(probs, cfg, ranks)
+    assert {p.rank for p in pieces} == set(range(ranks))
+    say(f"{name}: {len(pieces)} pieces over {ranks} ranks")
+    dw.poison_d()
+    for r in range(ranks):
+        share = [api.shard_problem(probs[p.problem], p) for p in pieces if p.rank == r]
+        assert api.run_grouped_gemm_once(share, SortMode.kByTiles, cfg) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dw.d.view(torch.int32), want.view(torch.int32)), "sharded D differs"
+    del want

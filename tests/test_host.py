@@ -272,3 +272,43 @@ def test_extreme_extents_stay_defined():
         # 2^30 macro-tiles each: the set's 2^31 no longer fits an int
         api.plan_launch([ProblemDesc(2**30, 2**13, 1, 1, 1, None, 1, 1, 2**13, 2**13, 2**13)] * 2, cfg, 256,
                         [1, 1, 1, 2, 2, 2])
+
+
+@pytest.mark.parametrize("name", ["mixed512", "dense64", "moe64", "longtail4096"])
+def test_shard_plan_matches_restatement(name):
+    """plan_shards splits a benchmark set across 1, 2, 3 and 8 ranks exactly as restated in
+    schedule_plan.py; every problem's columns are covered once, in order, cut only at 256-column
+    work-tile boundaries; dense64's 64 equal problems go 8 to each of 8 ranks; moe64's largest expert
+    is cut across ranks at 8."""
+    import schedule_plan as S
+    from grouped_gemm_gpu_kernel_amd.workloads import make_spec
+    spec = make_spec(name)
+    cfg = KernelConfig.named(spec.config)
+    probs = _problems(spec.m, spec.n, spec.k)
+    for ranks in (1, 2, 3, 8):
+        got = api.plan_shards(probs, cfg, ranks)
+        want = S.plan_shards([(p.m, p.n, p.k, p.c is not None and p.beta != 0.0) for p in probs], ranks, 256, 256, 64)
+        assert [(p.problem, p.rank, p.col0, p.cols) for p in got] == want, (name, ranks)
+        assert len(got) <= len(probs) + ranks
+        by_problem = {}
+        for p in got:
+            assert 0 <= p.rank < ranks and p.col0 % 256 == 0
+            by_problem.setdefault(p.problem, []).append(p)
+        assert sorted(by_problem) == list(range(len(probs)))
+        for i, ps in by_problem.items():
+            assert ps[0].col0 == 0 and sum(p.cols for p in ps) == max(probs[i].n, 0)
+            assert all(a.col0 + a.cols == b.col0 for a, b in zip(ps, ps[1:]))
+        if name == "dense64" and ranks == 8:
+            assert sorted(p.rank for p in got) == sorted(list(range(8)) * 8)
+        if name == "moe64" and ranks == 8:
+            big = int(np.argmax(spec.m))
+            assert len({p.rank for p in by_problem[big]}) > 1
+    with pytest.raises(Exception):
+        api.plan_shards(probs, cfg, 0)
+
+
+def test_shard_problem_offsets():
+    p = ProblemDesc(300, 1000, 70, 0x1000, 0x20000, 0x300000, 0x4000000, 70, 1000, 1000, 1000, 1.5, 0.5)
+    q = api.shard_problem(p, api.ShardPiece(0, 1, 512, 488))
+    assert (q.m, q.n, q.k, q.a, q.b, q.c, q.d) == (300, 488, 70, 0x1000, 0x20000 + 1024, 0x300000 + 2048, 0x4000000 + 2048)
+    assert (q.lda, q.ldb, q.ldc, q.ldd, q.alpha, q.beta) == (70, 1000, 1000, 1000, 1.5, 0.5)

@@ -19,16 +19,17 @@
 
 namespace {
 
+// The prepare runs in one workgroup with one thread per expert: 1024 threads, or one wave for
+// groups of at most 64 experts (no cross-wave scans; its barriers cost next to nothing).
 constexpr int kThreads = 1024;
 constexpr int kWave = 64;
-constexpr int kWaves = kThreads / kWave;
 constexpr int kChunks = GGK_SCHEDULER_CHUNKS;
 constexpr int kMaxExperts = GGK_MOE_MAX_EXPERTS;
 static_assert(kMaxExperts <= kThreads, "one thread per expert");
 static_assert(kMaxExperts % 4 == 0, "per-expert arrays are read four entries at a time");
 typedef int int4v __attribute__((ext_vector_type(4)));
 typedef double double2v __attribute__((ext_vector_type(2)));
-static_assert(kWaves <= kWave, "wave totals are scanned by one wave");
+static_assert(kThreads / kWave <= kWave, "wave totals are scanned by one wave");
 static_assert(2 + kChunks < GGK_MOE_STATUS && GGK_MOE_STATUS < GGK_MOE_HEADER_INTS, "header layout");
 
 struct MoeArgs {
@@ -80,10 +81,11 @@ __device__ __forceinline__ void least_from(unsigned long long& v, int& idx) {
   idx = take ? pidx : idx;
 }
 
-// Exclusive prefix sum of one value per thread over the workgroup, in thread
-// order; *total receives the sum.  Every thread must call it.
-template <class T>
+// Exclusive prefix sum of one value per thread over the workgroup of THREADS
+// threads, in thread order; *total receives the sum.  Every thread must call it.
+template <int THREADS, class T>
 __device__ T block_exclusive_scan(T v, T* s_waves, T* total) {
+  constexpr int kWaves = THREADS / kWave;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   T x = v;
@@ -93,6 +95,12 @@ __device__ T block_exclusive_scan(T v, T* s_waves, T* total) {
   }
   T before_lane = __shfl_up(x, 1, kWave);
   if (lane == 0) before_lane = T(0);
+  if constexpr (kWaves == 1) {
+    *total = __shfl(x, kWave - 1, kWave);
+    // Callers rely on the scan as a barrier for their shared-memory traffic around it.
+    __syncthreads();
+    return before_lane;
+  }
   if (lane == kWave - 1) s_waves[wave] = x;
   __syncthreads();
   if (wave == 0) {
@@ -110,7 +118,9 @@ __device__ T block_exclusive_scan(T v, T* s_waves, T* total) {
   return before_wave + before_lane;
 }
 
-__global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void moe_prepare_kernel(MoeArgs args) {
+  constexpr int kWaves = THREADS / kWave;
   __shared__ long long s_waves_ll[kWaves];
   __shared__ int s_waves_i[kWaves];
   __shared__ __attribute__((aligned(16))) int s_rows[kMaxExperts];
@@ -147,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
     }
   }
   long long all_rows;
-  const long long row0 = block_exclusive_scan<long long>(count, s_waves_ll, &all_rows);
+  const long long row0 = block_exclusive_scan<THREADS, long long>(count, s_waves_ll, &all_rows);
   const int tiles_n = L.n > 0 ? (L.n + args.cta_n - 1) / args.cta_n : 0;
   if (tid < experts) {
     const long long room = (long long)L.max_rows - row0;
@@ -205,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
                      : 0;
   }
   int total_tiles;
-  const int tile_off = block_exclusive_scan<int>(tiles, s_waves_i, &total_tiles);
+  const int tile_off = block_exclusive_scan<THREADS, int>(tiles, s_waves_i, &total_tiles);
   const bool reads_c = L.c != nullptr && L.beta != 0.0f;
   if (pos < experts) {
     args.offsets[pos] = tile_off;
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   }
   // At most GGK_MOE_MAX_EXPERTS (2^10) totals of at most 2^52: the sum is exact.
   long long sum_all;
-  (void)block_exclusive_scan<long long>(total, s_waves_ll, &sum_all);
+  (void)block_exclusive_scan<THREADS, long long>(total, s_waves_ll, &sum_all);
   const long long share = sum_all / kChunks + (sum_all % kChunks != 0 ? 1 : 0);
   if (pos < experts) {
     int rank = 0;
@@ -377,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void moe_prepare_kernel(MoeArgs args) {
   int sched_work = 0;
   if (pos < experts) sched_work = s_work[s_order[pos]];
   int total_work;
-  const int work_off = block_exclusive_scan<int>(sched_work, s_waves_i, &total_work);
+  const int work_off = block_exclusive_scan<THREADS, int>(sched_work, s_waves_i, &total_work);
   if (pos < experts) {
     args.order[pos] = s_order[pos];
     args.offsets[experts + 1 + pos] = work_off;
@@ -496,6 +506,10 @@ extern "C" hipError_t ggk_moe_prepare(int variant, int path, const ggk_moe_layou
   MoeArgs args{L,         d_counts,  sort_mode,  cta_m, cta_n, work.tiles_m, work.tiles_n, work.stage_k, d_problems,
                d_offsets, d_sorted_to_original, d_order, d_header};
   void* params[] = {&args};
-  return hipLaunchKernel(reinterpret_cast<const void*>(moe_prepare_kernel), dim3(1), dim3(kThreads), params, 0,
-                         stream);
+  if (L.experts <= kWave) {
+    return hipLaunchKernel(reinterpret_cast<const void*>(moe_prepare_kernel<kWave>), dim3(1), dim3(kWave), params, 0,
+                           stream);
+  }
+  return hipLaunchKernel(reinterpret_cast<const void*>(moe_prepare_kernel<kThreads>), dim3(1), dim3(kThreads), params,
+                         0, stream);
 }

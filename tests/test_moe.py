@@ -127,7 +127,7 @@ def _read_device_set(plan, experts):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("config", ["64x64x16", "128x64x32", "64x128x32"])
-@pytest.mark.parametrize("experts", [1, 5, 64, 256, 1024])
+@pytest.mark.parametrize("experts", [1, 5, 64, 65, 256, 1024])
 def test_device_prepare_equals_host_prepare(torch_cuda, config, experts):
     cfg = KernelConfig.named(config)
     rows = 3000
